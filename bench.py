@@ -1,0 +1,324 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X contraction / permutation hot path.
+
+Prints ONE JSON line. The headline (`value`) is fp32 contraction TFLOP/s on the north-star
+workload, C[4096,4096] = A[4096,4096] . B[4096,4096] row-major (a "step" is one such
+contraction over resident HBM inputs). The same line carries the permutation headline
+(GB/s on the 1 GiB-traffic [512,1024,256] perm (2,0,1) materialization) and every
+BASELINE configuration, each with its roofline fraction:
+  contraction: achieved = 2*B*M*N*K / mean kernel time, peak = 157.3 TFLOP/s fp32 MFMA
+  permutation: achieved = 2*numel*4 B / mean kernel time,  peak = 8000 GB/s HBM
+Kernel time is measured with HIP events recorded on the stream the kernels are launched on,
+around `steps` back-to-back launches after `warmup` untimed ones, with the stream synchronized
+on both sides. The CPU baseline times the C restatement of crates/cpu on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "pipeline-parallelism-deep-learning-library_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "contraction TFLOP/s (% fp32 MFMA peak); permute GB/s (% HBM peak)"
+PEAK_TFLOPS = 157.3     # MI355X dense fp32 MFMA
+PEAK_GBS = 8000.0       # MI355X HBM3E
+
+
+class HipEvents:
+    """hipEvent timing on a given stream (the library's own stream)."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def new(self):
+        ev = ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(ev)) == 0
+        return ev
+
+    def record(self, ev, stream):
+        assert self.hip.hipEventRecord(ev, stream) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return float(ms.value)
+
+
+def timed(ctx, events, launch, steps, warmup):
+    """Mean ms per launch over `steps` launches, bracketed by stream syncs."""
+    for _ in range(warmup):
+        launch()
+    ctx.sync()
+    s = ctx.queue.handle
+    e0, e1 = events.new(), events.new()
+    events.record(e0, s)
+    for _ in range(steps):
+        launch()
+    events.record(e1, s)
+    total = events.elapsed_ms(e0, e1)
+    ctx.sync()
+    return total / steps
+
+
+def upload(pool, L, data: np.ndarray):
+    buf = pool.alloc("f32", data.size)
+    buf.write(data)
+    return buf
+
+
+def bench_gemm(ctx, events, pool, L, C, name, m, n, k, args, a_t=False, b_t=False, batch=1,
+               seed=(12, 13), sigma=None, beta=0.0):
+    g = np.random.Generator(np.random.PCG64(seed[0]))
+    h = np.random.Generator(np.random.PCG64(seed[1]))
+    if sigma is None:
+        a = g.uniform(-1, 1, batch * m * k).astype(np.float32)
+        b = h.uniform(-1, 1, batch * k * n).astype(np.float32)
+    else:
+        a = (g.standard_normal(batch * m * k) * sigma).astype(np.float32)
+        b = (h.standard_normal(batch * k * n) * sigma).astype(np.float32)
+    A, B = upload(pool, L, a), upload(pool, L, b)
+    Cb = pool.alloc("f32", batch * m * n)
+    bs = [] if batch == 1 else [batch]
+    av = (L.TensorView(A, 0, bs + [m, k], ([m * k] if bs else []) + [1, m]) if a_t
+          else L.TensorView.row_major(A, 0, bs + [m, k]))
+    bv = (L.TensorView(B, 0, bs + [k, n], ([k * n] if bs else []) + [1, k]) if b_t
+          else L.TensorView.row_major(B, 0, bs + [k, n]))
+    cv = L.TensorView.row_major(Cb, 0, bs + [m, n])
+    plan = C.plan_gemm(1.0, av, bv, beta, cv)
+    ms = timed(ctx, events, lambda: C.encode_gemm(ctx, ctx.queue, 1.0, av, bv, beta, cv),
+               args.steps, args.warmup)
+    flops = 2.0 * batch * m * n * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"name": name, "ms": ms, "tflops": tflops, "frac": tflops / PEAK_TFLOPS,
+            "plan": {k_: plan[k_] for k_ in ("kind", "a_mode", "b_mode", "splits", "workgroups")},
+            "_host": (a, b)}
+
+
+def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
+    n = int(np.prod(shape))
+    x = np.random.Generator(np.random.PCG64(seed)).uniform(-1, 1, n).astype(np.float32)
+    src_buf = upload(pool, L, x)
+    dst_buf = pool.alloc("f32", n)
+    src = P.permute_view(L.TensorView.row_major(src_buf, 0, shape), perm)
+    dst = L.TensorView.row_major(dst_buf, 0, src.shape)
+    plan = P.plan("materialize", src, dst)
+    ms = timed(ctx, events, lambda: P.encode_materialize(ctx, ctx.queue, src, dst), args.steps,
+               args.warmup)
+    gbs = 2.0 * n * 4 / (ms * 1e-3) / 1e9
+    return {"name": name, "ms": ms, "gbs": gbs, "frac": gbs / PEAK_GBS,
+            "plan": {k_: plan[k_] for k_ in ("kind", "vector", "workgroups", "shape")},
+            "_host": x}
+
+
+def bench_copy(ctx, events, pool, L, P, n, args):
+    """A plain 128-bit copy through the same library (contiguous materialize)."""
+    src_buf = pool.alloc("f32", n)
+    dst_buf = pool.alloc("f32", n)
+    src = L.TensorView.row_major(src_buf, 0, [n])
+    dst = L.TensorView.row_major(dst_buf, 0, [n])
+    ms = timed(ctx, events, lambda: P.encode_materialize(ctx, ctx.queue, src, dst), args.steps,
+               args.warmup)
+    return 2.0 * n * 4 / (ms * 1e-3) / 1e9
+
+
+def traffic_from_profile(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic_<name>.txt)."""
+    p = REPO / "profiles" / f"traffic_{name}.txt"
+    if not p.exists():
+        return None
+    vals = {}
+    for line in p.read_text().splitlines():
+        if "=" in line and not line.startswith("#"):
+            key, val = line.split("=", 1)
+            vals[key.strip()] = val.strip()
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baselines(gemm_host, perm_host, args):
+    """crates/cpu restated (oracle/), timed on bounded samples of the same workloads."""
+    import oracle
+    out = {}
+    a, b = gemm_host
+    n = 4096
+    # Literal single-thread accumulation (what crates/cpu runs): a sample of output rows.
+    rows = np.arange(2, dtype=np.uint64)
+    c = np.zeros(n * n, np.float32)
+    t0 = time.perf_counter()
+    for r in rows:
+        oracle.gemm_seq(1, n, n, 1.0, 0.0, a, int(r) * n, (n, 1), b, 0, (n, 1), c, int(r) * n, (n, 1))
+    dt = time.perf_counter() - t0
+    flops = 2.0 * len(rows) * n * n
+    out["gemm_seq"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                       "sample": f"{len(rows)} of 4096 output rows of the 4096^3 gemm, "
+                                 f"literal k-order loop ({dt:.1f} s)"}
+    threads = min(os.cpu_count() or 1, 16)
+    rows = np.arange(128, dtype=np.uint64)
+    t0 = time.perf_counter()
+    oracle.gemm_fast(n, n, n, 1.0, 0.0, a, 0, (n, 1), b, 0, (n, 1), c, 0, (n, 1), rows=rows,
+                     threads=threads)
+    dt = time.perf_counter() - t0
+    flops = 2.0 * len(rows) * n * n
+    out["gemm_fast"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
+                        "kind": "port",
+                        "sample": f"{len(rows)} of 4096 output rows, bit-identical loop-interchanged "
+                                  f"variant on {threads} threads ({dt:.1f} s)"}
+    x = perm_host
+    shape, perm = [512, 1024, 256], [2, 0, 1]
+    # gather_words over the first 32 of 256 output planes (dst[c] = src[:, :, c]).
+    sample_planes = 32
+    t0 = time.perf_counter()
+    words = x.view(np.uint32)
+    oracle.gather_words(words, 1, 0, [sample_planes, 512, 1024], [1, 1024 * 256, 256])
+    dt = time.perf_counter() - t0
+    nbytes = 2.0 * sample_planes * 512 * 1024 * 4
+    out["permute"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                      "sample": f"gather_words of {sample_planes} of 256 output planes of "
+                                f"[512,1024,256] perm (2,0,1) ({dt:.1f} s)"}
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default=None,
+                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import linalg_hip as L
+    from linalg_hip import contraction as C
+    from linalg_hip import permutation as P
+    sys.path.insert(0, str(REPO / "tests"))
+
+    ctx = L.Context.new(0)
+    events = HipEvents()
+
+    class Pool:
+        def __init__(self):
+            self.b = []
+
+        def alloc(self, dt, n):
+            buf = L.alloc_shared(ctx, dt, n)
+            self.b.append(buf)
+            return buf
+
+        def free(self):
+            for x in self.b:
+                x.free()
+            self.b = []
+
+    pool = Pool()
+    only = args.only
+    results = {}
+
+    def run(name, fn):
+        if only is None or only == name:
+            print(f"[bench] {name} ...", file=sys.stderr, flush=True)
+            results[name] = fn()
+            pool.free()
+
+    run("gemm4096", lambda: bench_gemm(ctx, events, pool, L, C, "gemm 4096^3", 4096, 4096, 4096, args))
+    run("c1", lambda: bench_gemm(ctx, events, pool, L, C, "C1 gemm 512^3", 512, 512, 512, args, seed=(1, 2)))
+    run("c3", lambda: bench_gemm(ctx, events, pool, L, C, "C3 bik,bkj->bij B=32 1024^3, B permuted",
+                                 1024, 1024, 1024, args, b_t=True, batch=32, seed=(5, 6)))
+    run("c4", lambda: bench_gemm(ctx, events, pool, L, C, "C4 split-K 256x256x65536", 256, 256, 65536,
+                                 args, seed=(7, 8), sigma=1.0 / 256))
+
+    def c5():
+        M, K, N = 4096, 4096, 16384
+        y = bench_gemm(ctx, events, pool, L, C, "C5 Y=X.W", M, N, K, args, seed=(9, 10), sigma=0.02)
+        pool.free()
+        dx = bench_gemm(ctx, events, pool, L, C, "C5 dX=dY.W^T", M, K, N, args, b_t=True,
+                        seed=(11, 10), sigma=0.02)
+        pool.free()
+        dw = bench_gemm(ctx, events, pool, L, C, "C5 dW=X^T.dY", K, N, M, args, a_t=True,
+                        seed=(9, 11), sigma=0.02, beta=1.0)
+        ms = y["ms"] + dx["ms"] + dw["ms"]
+        tf = 3 * 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        for r in (y, dx, dw):
+            r.pop("_host")
+        return {"name": "C5 linear-layer step (3 gemms)", "ms": ms, "tflops": tf,
+                "frac": tf / PEAK_TFLOPS, "parts": [y, dx, dw]}
+    run("c5", c5)
+    run("c2a", lambda: bench_perm(ctx, events, pool, L, P, "C2a [64,128,64,32] perm (0,2,3,1)",
+                                  [64, 128, 64, 32], [0, 2, 3, 1], 3, args))
+    run("c2b", lambda: bench_perm(ctx, events, pool, L, P, "C2b [512,1024,256] perm (2,0,1)",
+                                  [512, 1024, 256], [2, 0, 1], 4, args))
+    run("copy", lambda: {"name": "plain 128-bit copy 512 MiB", "gbs": bench_copy(ctx, events, pool,
+                                                                                 L, P, 1 << 27, args)})
+
+    gemm_host = results.get("gemm4096", {}).pop("_host", None)
+    perm_host = results.get("c2b", {}).pop("_host", None)
+    for r in results.values():
+        if isinstance(r, dict):
+            r.pop("_host", None)
+
+    cpu = None
+    if not args.no_cpu and gemm_host is not None and perm_host is not None:
+        cpu = cpu_baselines(gemm_host, perm_host, args)
+
+    head = results.get("gemm4096")
+    perm = results.get("c2b")
+    line = {"metric": METRIC, "value": round(head["tflops"], 3) if head else None,
+            "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(head["ms"], 4) if head else None, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "fp32 contraction C[4096,4096] = A.B row-major (north-star "
+                                   "4096^3); permutation headline [512,1024,256] perm (2,0,1)",
+                       "m": 4096, "n": 4096, "k": 4096, "parallelism": "single-gpu"}}
+    if head:
+        line["roofline"] = {"bound": "mfma", "achieved": round(head["tflops"], 3),
+                            "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(head["frac"], 4),
+                            "traffic": traffic_from_profile("gemm4096"),
+                            "kernel": "gemm_f32_mfma<K,MN>",
+                            "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
+    if cpu:
+        line["cpu_baseline"] = cpu["gemm_seq"]
+        line["cpu_baseline_parallel"] = cpu["gemm_fast"]
+    if perm:
+        line["permute"] = {"value": round(perm["gbs"], 1), "unit": "GB/s",
+                           "workload": perm["name"], "ms_per_step": round(perm["ms"], 4),
+                           "roofline": {"bound": "hbm", "achieved": round(perm["gbs"], 1),
+                                        "peak": PEAK_GBS, "unit": "GB/s",
+                                        "frac": round(perm["frac"], 4),
+                                        "traffic": traffic_from_profile("c2b"),
+                                        "kernel": "perm_tile_w1_v128",
+                                        "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
+                           "cpu_baseline": cpu["permute"] if cpu else None}
+    line["configs"] = {k_: {kk: (round(v, 4) if isinstance(v, float) else v)
+                            for kk, v in r.items()} for k_, r in results.items()}
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,265 @@
+/*
+ * linalg_hip.h — C ABI of the MI355X (gfx950) tensor-contraction and permutation backend.
+ *
+ * This is the drop-in boundary for the reference's L1 operator surface
+ * (`linalg::ops::contraction`, `linalg::ops::permutation`) and its L0 data model
+ * (`linalg::abi`). Every entry point below names the reference item it replaces
+ * (paths relative to the reference repository root).
+ *
+ * Conventions
+ *  - Plain C types only: pointers, fixed-width integers, floats. No HIP or torch types;
+ *    streams travel as `void*` (a `hipStream_t`), NULL meaning the context's own stream.
+ *  - Views are in ELEMENTS: the element at multi-index idx lives at element
+ *    `offset + sum(idx[d] * strides[d])` counted from `base`, exactly as
+ *    `TensorView` (src/abi.rs:64-76). `base` is always the allocation base returned by
+ *    lg_alloc (never an offset-adjusted pointer) and `bytes` its length, which play the
+ *    roles of `buffer.contents()` and `buffer.length()`.
+ *  - Every call validates everything first. On any error it launches nothing and writes
+ *    nothing, returns a non-zero lg_status, and lg_last_error() describes the failure
+ *    (src/ops/contraction.rs:1024-1035, src/ops/permutation.rs:163-198). Nothing aborts
+ *    on bad metadata.
+ *  - `lg_encode_*` only enqueue on the given stream (the reference's `encode_*` into a
+ *    command buffer); the un-prefixed forms enqueue on the context stream and wait for
+ *    completion (the reference's synchronous `contract`, `gemm`, `materialize`, ...).
+ *    Enqueue order on one stream is execution order.
+ *  - Thread safety: calls on different streams may run concurrently. As in
+ *    crates/core/src/lib.rs:67-70, the caller must not let two in-flight calls write
+ *    overlapping memory.
+ */
+#ifndef LINALG_HIP_H
+#define LINALG_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Largest rank a view may carry. The reference's TensorView holds a Vec of any length;
+ * 16 is far beyond every caller of the hot path. */
+#define LG_MAX_RANK 16
+/* Allocation granularity of lg_alloc, as ALLOC_GRANULE (src/abi.rs:221-223). */
+#define LG_ALLOC_GRANULE 16384u
+
+/* Status codes: LinalgError (src/abi.rs:20-33). */
+typedef enum lg_status {
+    LG_OK = 0,
+    LG_NO_DEVICE = 1,        /* LinalgError::NoDevice */
+    LG_INVALID_ARGUMENT = 2, /* LinalgError::InvalidArgument */
+    LG_OVERLAP = 3,          /* LinalgError::Overlap */
+    LG_KERNEL = 4            /* LinalgError::ShaderCompile: code-object, launch or runtime failure */
+} lg_status;
+
+/* Element types the permutation kernels move as raw bits
+ * (permutation::Element, src/ops/permutation.rs:26-54). Contraction is f32-only here. */
+typedef enum lg_elem {
+    LG_ELEM_F32 = 0, /* one 32-bit word */
+    LG_ELEM_U32 = 1, /* one 32-bit word */
+    LG_ELEM_I32 = 2, /* one 32-bit word */
+    LG_ELEM_C32 = 3  /* complex f32 [re, im]: two words; conjugation flips the sign bit of im */
+} lg_elem;
+
+/* A strided window into one allocation (TensorView, src/abi.rs:64-76).
+ * `rank` entries of `shape` and `nstrides` entries of `strides` are meaningful; they must be
+ * equal for the view to validate (the reference's "rank mismatch" check). */
+typedef struct lg_view {
+    void* base;                      /* allocation base (device memory) */
+    uint64_t bytes;                  /* allocation length in bytes */
+    uint64_t offset;                 /* in elements */
+    uint32_t rank;                   /* number of axes in `shape` */
+    uint32_t nstrides;               /* number of entries in `strides` */
+    uint64_t shape[LG_MAX_RANK];     /* extents */
+    uint64_t strides[LG_MAX_RANK];   /* in elements */
+} lg_view;
+
+/* ---------------------------------------------------------------------------------------
+ * Errors
+ * ------------------------------------------------------------------------------------- */
+
+/* Message of the last failing call on this thread ("" if none). The LinalgError payload
+ * (src/abi.rs:24-43). Valid until the next call on the same thread. */
+const char* lg_last_error(void);
+
+/* ---------------------------------------------------------------------------------------
+ * Context and memory (src/abi.rs:51-62, 221-243)
+ * ------------------------------------------------------------------------------------- */
+
+typedef struct lg_ctx lg_ctx;
+
+/* Opens HIP device `device` and creates one stream on it: MetalContext::new
+ * (src/abi.rs:55-61). LG_NO_DEVICE when no such device exists. */
+lg_status lg_ctx_create(int32_t device, lg_ctx** out);
+/* Waits for the context stream, then releases it. NULL is ignored. */
+void lg_ctx_destroy(lg_ctx* ctx);
+/* The context's hipStream_t (MetalContext::queue). */
+void* lg_ctx_stream(const lg_ctx* ctx);
+/* Blocks until all work enqueued on the context stream has completed
+ * (`wait_until_completed`, src/ops/contraction.rs:1015-1022). */
+lg_status lg_ctx_sync(lg_ctx* ctx);
+/* Blocks until all work on `stream` (a hipStream_t; NULL = context stream) has completed. */
+lg_status lg_stream_sync(lg_ctx* ctx, void* stream);
+/* A new stream on the context's device: the analogue of `queue.new_command_buffer()`
+ * that the reference's `encode_*` calls fill (src/ops/contraction.rs:1057-1063). Work
+ * enqueued on it starts without an explicit commit. */
+lg_status lg_stream_create(lg_ctx* ctx, void** stream);
+/* Waits for `stream` and destroys it. */
+lg_status lg_stream_destroy(lg_ctx* ctx, void* stream);
+
+/* Zero-filled device allocation holding at least `len` elements of `elem_bytes` bytes,
+ * rounded up to whole LG_ALLOC_GRANULE granules (at least one, so len = 0 is legal):
+ * alloc_shared (src/abi.rs:225-243). MI355X memory is not host-visible, so contents move
+ * with lg_upload / lg_download. */
+lg_status lg_alloc(lg_ctx* ctx, uint64_t elem_bytes, uint64_t len, void** base, uint64_t* bytes);
+/* Frees an lg_alloc allocation after the context stream has drained. */
+lg_status lg_free(lg_ctx* ctx, void* base);
+/* Host -> device copy of `nbytes` at byte offset `byte_offset` of allocation `base`,
+ * ordered after all earlier work on the context stream; returns once complete. */
+lg_status lg_upload(lg_ctx* ctx, void* base, uint64_t byte_offset, const void* src, uint64_t nbytes);
+/* Device -> host copy, ordered after all earlier work on the context stream. */
+lg_status lg_download(lg_ctx* ctx, const void* base, uint64_t byte_offset, void* dst, uint64_t nbytes);
+
+/* ---------------------------------------------------------------------------------------
+ * View metadata (host only, no device work)
+ * ------------------------------------------------------------------------------------- */
+
+/* TensorView::validate (src/abi.rs:140-177) for elements of `elem_bytes` bytes. */
+lg_status lg_view_validate(const lg_view* view, uint32_t elem_bytes);
+/* TensorView::may_overlap (src/abi.rs:193-204): 1 when both views live in the same
+ * allocation and their byte ranges intersect, else 0. Views must have validated. */
+int32_t lg_view_may_overlap(const lg_view* a, uint32_t a_elem_bytes, const lg_view* b,
+                            uint32_t b_elem_bytes);
+
+/* ---------------------------------------------------------------------------------------
+ * Permutation (src/ops/permutation.rs:272-387)
+ * ------------------------------------------------------------------------------------- */
+
+/* permute_view (src/ops/permutation.rs:295-320): axis i of *out is axis perm[i] of *view.
+ * Metadata only. LG_INVALID_ARGUMENT unless perm is a permutation of 0..rank. */
+lg_status lg_permute_view(const lg_view* view, const uint64_t* perm, uint32_t perm_len,
+                          lg_view* out);
+
+/* encode_materialize / materialize (src/ops/permutation.rs:322-342): copies `src` (any
+ * strided view) into the contiguous row-major `dst` of the same shape, bit for bit. */
+lg_status lg_encode_materialize(lg_ctx* ctx, void* stream, lg_elem elem, const lg_view* src,
+                                const lg_view* dst);
+lg_status lg_materialize(lg_ctx* ctx, lg_elem elem, const lg_view* src, const lg_view* dst);
+
+/* encode_conjugate / conjugate (src/ops/permutation.rs:344-369): as materialize, flipping
+ * the sign bit of the imaginary word of complex elements (a plain copy for real types). */
+lg_status lg_encode_conjugate(lg_ctx* ctx, void* stream, lg_elem elem, const lg_view* src,
+                              const lg_view* dst);
+lg_status lg_conjugate(lg_ctx* ctx, lg_elem elem, const lg_view* src, const lg_view* dst);
+
+/* encode_adjoint / adjoint (src/ops/permutation.rs:371-387): swaps the last two axes of
+ * `src` (rank >= 2) and conjugates complex elements into the row-major `dst`. */
+lg_status lg_encode_adjoint(lg_ctx* ctx, void* stream, lg_elem elem, const lg_view* src,
+                            const lg_view* dst);
+lg_status lg_adjoint(lg_ctx* ctx, lg_elem elem, const lg_view* src, const lg_view* dst);
+
+/* ---------------------------------------------------------------------------------------
+ * Contraction (src/ops/contraction.rs:1024-1130), f32
+ * ------------------------------------------------------------------------------------- */
+
+/* encode_contract / contract (src/ops/contraction.rs:1036-1064):
+ *   C = alpha * A.B + beta * C over einsum labels (one ASCII byte per axis).
+ * A label in A and B but not C is contracted; A and C: an M axis; B and C: an N axis; all
+ * three: a batch axis. beta = 0 never reads C, alpha = 0 never reads A or B, K = 0 gives
+ * C = beta * C, an empty M, N or batch launches nothing. LG_OVERLAP when C aliases an input
+ * it reads or writes an element twice (the in-place scale with the other extents 1 is
+ * allowed). */
+lg_status lg_encode_contract_f32(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                 const char* a_labels, const lg_view* b, const char* b_labels,
+                                 float beta, const lg_view* c, const char* c_labels);
+lg_status lg_contract_f32(lg_ctx* ctx, float alpha, const lg_view* a, const char* a_labels,
+                          const lg_view* b, const char* b_labels, float beta, const lg_view* c,
+                          const char* c_labels);
+
+/* encode_gemm / gemm / gemm_nowait (src/ops/contraction.rs:1066-1130): batched matrix form.
+ * Equal ranks r >= 2; leading r-2 axes are batch; A[..., M, K], B[..., K, N], C[..., M, N].
+ * Strides may describe transposes or windows; nothing is copied. gemm_nowait enqueues on
+ * the context stream and returns without waiting. */
+lg_status lg_encode_gemm_f32(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                             const lg_view* b, float beta, const lg_view* c);
+lg_status lg_gemm_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b, float beta,
+                      const lg_view* c);
+lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b,
+                             float beta, const lg_view* c);
+
+/* ---------------------------------------------------------------------------------------
+ * Plan inspection (host only; no context, no device work). These run the exact
+ * validation and planning of the entry points above and report the plan instead of
+ * launching it, so the planner is testable without a GPU.
+ * ------------------------------------------------------------------------------------- */
+
+/* Plan kinds of a contraction (Plan, src/ops/contraction.rs:664-675). */
+typedef enum lg_plan_kind {
+    LG_PLAN_EMPTY = 0,   /* nothing to do */
+    LG_PLAN_ZERO = 1,    /* Fill with beta = 0: C = 0 without reading C */
+    LG_PLAN_SCALE = 2,   /* Fill with beta != 0: C = beta * C */
+    LG_PLAN_TILED = 3,   /* one MFMA GEMM launch */
+    LG_PLAN_SPLIT = 4,   /* split-K MFMA partials + ordered reduction */
+    LG_PLAN_GENERAL = 5  /* mixed-radix fallback (more than one stride per group) */
+} lg_plan_kind;
+
+/* Operand load modes of the tiled kernel. */
+typedef enum lg_load_mode {
+    LG_LOAD_K_CONTIG = 0,  /* unit stride along K: 128-bit loads along K */
+    LG_LOAD_MN_CONTIG = 1, /* unit stride along M (A) or N (B): 128-bit loads along M/N */
+    LG_LOAD_STRIDED = 2    /* neither, or misaligned: 32-bit predicated loads */
+} lg_load_mode;
+
+typedef struct lg_contract_plan {
+    uint32_t kind;        /* lg_plan_kind */
+    uint32_t a_mode;      /* lg_load_mode of A (tiled/split) */
+    uint32_t b_mode;      /* lg_load_mode of B (tiled/split) */
+    uint32_t groups;      /* max number of strides in any merged group */
+    uint64_t batch, m, n, k;
+    uint64_t splits;      /* 1 unless LG_PLAN_SPLIT */
+    uint64_t k_chunk;     /* K elements per split */
+    uint64_t workgroups;  /* workgroups of the main launch */
+    uint64_t scratch_bytes; /* device scratch of the split-K partials */
+} lg_contract_plan;
+
+lg_status lg_plan_contract_f32(float alpha, const lg_view* a, const char* a_labels,
+                               const lg_view* b, const char* b_labels, float beta,
+                               const lg_view* c, const char* c_labels, lg_contract_plan* out);
+lg_status lg_plan_gemm_f32(float alpha, const lg_view* a, const lg_view* b, float beta,
+                           const lg_view* c, lg_contract_plan* out);
+
+/* Permutation plan (encode_gather's path choice, src/ops/permutation.rs:200-268). */
+typedef enum lg_permute_kind {
+    LG_PERMUTE_EMPTY = 0, /* nothing to move */
+    LG_PERMUTE_COPY = 1,  /* gather with contiguous 128-bit writes */
+    LG_PERMUTE_TILE = 2   /* LDS-tiled 2-axis transpose, 128-bit reads and writes */
+} lg_permute_kind;
+
+typedef struct lg_permute_plan {
+    uint32_t kind;          /* lg_permute_kind */
+    uint32_t rank;          /* rank after coalescing */
+    uint32_t axis_a;        /* tile: source unit-stride axis */
+    uint32_t axis_b;        /* tile: destination unit-stride axis (rank - 1) */
+    uint32_t vector;        /* 1 when the 128-bit path is legal (alignment) */
+    uint32_t conj;          /* 1 when the imaginary sign bit is flipped */
+    uint64_t shape[8];      /* coalesced extents */
+    uint64_t strides[8];    /* coalesced source strides */
+    uint64_t workgroups;    /* workgroups of the launch */
+} lg_permute_plan;
+
+/* `op`: 0 materialize, 1 conjugate, 2 adjoint. */
+lg_status lg_plan_permute(uint32_t op, lg_elem elem, const lg_view* src, const lg_view* dst,
+                          lg_permute_plan* out);
+
+/* ---------------------------------------------------------------------------------------
+ * Debug counters (the reference's debug launch log, crates/cpu/src/lib.rs:79-148)
+ * ------------------------------------------------------------------------------------- */
+
+/* Number of kernels this context has launched. */
+uint64_t lg_debug_launch_count(const lg_ctx* ctx);
+/* Name of launch `i` counted from 0, for the last 256 launches; NULL if out of range. */
+const char* lg_debug_launch_name(const lg_ctx* ctx, uint64_t i);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LINALG_HIP_H */

@@ -1,0 +1,189 @@
+"""CPU oracle for the contraction / permutation hot path (test infrastructure only).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+package, and only as the checker or the timed CPU baseline. The product
+(liblinalg_hip.so) never routes through it.
+
+Functions (C implementations in oracle.c, each citing the reference code it restates):
+  gemm_seq        CpuBackend::gemm accumulation, literal single-thread form
+                  (crates/cpu/src/lib.rs:203-295, 606-691)
+  gemm_fast       the same arithmetic, loop-interchanged and multi-threaded; bit-identical
+  gather_words    tests/permutation_test.rs:84-116
+  contract_f64    tests/contraction_test.rs:200-268 (f64 accumulation, error magnitude)
+  gate            tests/contraction_test.rs:280-313 accuracy gate
+  north_star_tol  max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+U = 2.0 ** -24          # unit roundoff of f32 (tests/contraction_test.rs:35-36)
+TINY_F32 = 1.401298464324817e-45
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            from . import build as _build
+            _build.build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        f32p = ctypes.POINTER(ctypes.c_float)
+        i64, u64 = ctypes.c_int64, ctypes.c_uint64
+        L.oracle_gemm_seq_f32.argtypes = [u64, u64, u64, ctypes.c_float, ctypes.c_float,
+                                          f32p, i64, i64, f32p, i64, i64, f32p, i64, i64]
+        L.oracle_gemm_seq_f32.restype = None
+        L.oracle_gemm_fast_f32.argtypes = [u64, u64, u64, ctypes.c_float, ctypes.c_float,
+                                           f32p, i64, i64, f32p, i64, i64, f32p, i64, i64,
+                                           ctypes.POINTER(u64), u64, ctypes.c_int]
+        L.oracle_gemm_fast_f32.restype = ctypes.c_int
+        L.oracle_gather_words.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32, u64,
+                                          ctypes.c_uint32, ctypes.POINTER(u64),
+                                          ctypes.POINTER(u64), ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_uint32)]
+        L.oracle_gather_words.restype = u64
+        dp = ctypes.POINTER(ctypes.c_double)
+        i64p = ctypes.POINTER(i64)
+        u64p = ctypes.POINTER(u64)
+        L.oracle_contract_f64.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_uint32, u64p,
+                                          i64p, i64p, i64p, ctypes.c_uint32, u64p, i64p, i64p,
+                                          f32p, u64, f32p, u64, f32p, u64, dp, dp, u64p]
+        L.oracle_contract_f64.restype = None
+        _lib = L
+    return _lib
+
+
+def _fp(arr: np.ndarray, offset: int = 0):
+    assert arr.dtype == np.float32
+    return ctypes.cast(arr.ctypes.data + 4 * offset, ctypes.POINTER(ctypes.c_float))
+
+
+def gemm_seq(m, n, k, alpha, beta, a, a_off, a_strides, b, b_off, b_strides, c, c_off, c_strides):
+    """Literal crates/cpu accumulation on flat float32 buffers (updated in place: c)."""
+    lib().oracle_gemm_seq_f32(m, n, k, alpha, beta, _fp(a, a_off), a_strides[0], a_strides[1],
+                              _fp(b, b_off), b_strides[0], b_strides[1], _fp(c, c_off),
+                              c_strides[0], c_strides[1])
+
+
+def gemm_fast(m, n, k, alpha, beta, a, a_off, a_strides, b, b_off, b_strides, c, c_off,
+              c_strides, rows=None, threads=None):
+    """Bit-identical multi-threaded form; `rows` restricts the computed rows."""
+    if threads is None:
+        threads = os.cpu_count() or 1
+    rp = None
+    nrows = 0
+    if rows is not None:
+        rows = np.ascontiguousarray(rows, dtype=np.uint64)
+        rp = rows.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
+        nrows = rows.size
+    rc = lib().oracle_gemm_fast_f32(m, n, k, alpha, beta, _fp(a, a_off), a_strides[0],
+                                    a_strides[1], _fp(b, b_off), b_strides[0], b_strides[1],
+                                    _fp(c, c_off), c_strides[0], c_strides[1], rp, nrows,
+                                    int(threads))
+    if rc != 0:
+        raise RuntimeError(f"oracle_gemm_fast_f32 failed ({rc})")
+
+
+def gather_words(words: np.ndarray, w: int, offset: int, shape, strides, conj=False,
+                 complex_elem=False) -> np.ndarray:
+    """Raw words of a view in row-major logical order (tests/permutation_test.rs:84-116)."""
+    words = np.ascontiguousarray(words, dtype=np.uint32)
+    n = int(np.prod(shape, dtype=np.uint64)) if len(shape) else 1
+    out = np.zeros(max(n * w, 1), dtype=np.uint32)
+    sh = (ctypes.c_uint64 * max(len(shape), 1))(*shape)
+    st = (ctypes.c_uint64 * max(len(strides), 1))(*strides)
+    got = lib().oracle_gather_words(words.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), w,
+                                    offset, len(shape), sh, st, int(conj), int(complex_elem),
+                                    out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    return out[:got]
+
+
+class Expected:
+    """exact / magnitude / index per logical element of C, and K (contraction_test.rs:186-197)."""
+
+    def __init__(self, exact, magnitude, index, k):
+        self.exact, self.magnitude, self.index, self.k = exact, magnitude, index, k
+
+
+def contract_f64(alpha, a, a_layout, a_labels, b, b_layout, b_labels, beta, c, c_layout,
+                 c_labels) -> Expected:
+    """f64 reference over labelled operands. Layouts are (offset, shape, strides)."""
+    extent = {}
+    for labels, (_, shape, _) in ((a_labels, a_layout), (b_labels, b_layout), (c_labels, c_layout)):
+        for l, n in zip(labels, shape):
+            assert extent.setdefault(l, n) == n, "test bug: extent mismatch"
+    free = list(c_labels)
+    summed = [l for l in a_labels if l in b_labels and l not in c_labels]
+
+    def strides_for(labels, layout, over):
+        _, _, st = layout
+        return [st[labels.index(l)] if l in labels else 0 for l in over]
+
+    u64a = lambda v: np.ascontiguousarray(v, dtype=np.uint64)
+    i64a = lambda v: np.ascontiguousarray(v, dtype=np.int64)
+    fe = u64a([extent[l] for l in free] or [1])
+    se = u64a([extent[l] for l in summed] or [1])
+    af, bf, cf = (i64a(strides_for(lbl, lay, free) or [0]) for lbl, lay in
+                  ((a_labels, a_layout), (b_labels, b_layout), (c_labels, c_layout)))
+    as_, bs_ = (i64a(strides_for(lbl, lay, summed) or [0]) for lbl, lay in
+                ((a_labels, a_layout), (b_labels, b_layout)))
+    nf = int(np.prod([extent[l] for l in free], dtype=np.int64)) if free else 1
+    k = int(np.prod([extent[l] for l in summed], dtype=np.int64)) if summed else 1
+    exact = np.zeros(nf, dtype=np.float64)
+    mag = np.zeros(nf, dtype=np.float64)
+    index = np.zeros(nf, dtype=np.uint64)
+    P = lambda arr, t: arr.ctypes.data_as(ctypes.POINTER(t))
+    lib().oracle_contract_f64(alpha, beta, len(free), P(fe, ctypes.c_uint64), P(af, ctypes.c_int64),
+                              P(bf, ctypes.c_int64), P(cf, ctypes.c_int64), len(summed),
+                              P(se, ctypes.c_uint64), P(as_, ctypes.c_int64), P(bs_, ctypes.c_int64),
+                              _fp(a), a_layout[0], _fp(b), b_layout[0], _fp(c), c_layout[0],
+                              P(exact, ctypes.c_double), P(mag, ctypes.c_double),
+                              P(index, ctypes.c_uint64))
+    if nf == 0:
+        k = k
+    return Expected(exact, mag, index.astype(np.int64), k)
+
+
+def gate(got_buffer: np.ndarray, expected: Expected, name: str = "") -> dict:
+    """tests/contraction_test.rs:280-313: |got - ref| <= (K+2)u*mag + u*|ref| + tiny, where ref
+    is the f64 result rounded once to f32; non-finite refs must match exactly (NaN ~ NaN).
+    Returns statistics; raises AssertionError on the first violation."""
+    k = float(expected.k)
+    if expected.index.size == 0:
+        return {"normalized": 0.0, "gate": 0.0, "max_err": 0.0}
+    value = got_buffer[expected.index].astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        rounded = expected.exact.astype(np.float32).astype(np.float64)
+    finite = np.isfinite(rounded)
+    bad_nf = ~finite & ~((value == rounded) | (np.isnan(value) & np.isnan(rounded)))
+    if bad_nf.any():
+        i = int(np.flatnonzero(bad_nf)[0])
+        raise AssertionError(f"{name}: element {i} is {value[i]}, expected {rounded[i]}")
+    with np.errstate(invalid="ignore"):
+        err = np.where(finite, np.abs(value - rounded), 0.0)
+    tol = (k + 2.0) * U * expected.magnitude + U * np.abs(np.where(finite, rounded, 0.0)) + TINY_F32
+    viol = finite & ~(err <= tol)
+    if viol.any():
+        i = int(np.flatnonzero(viol)[0])
+        raise AssertionError(f"{name}: element {i} is {value[i]}, expected {rounded[i]} "
+                             f"(exact {expected.exact[i]}); error {err[i]:e} exceeds {tol[i]:e}, K={k}")
+    max_err = float(err.max()) if err.size else 0.0
+    return {"normalized": max_err / (max(k, 1.0) ** 0.5 * U),
+            "gate": float((err / tol).max()) if err.size else 0.0,
+            "max_err": max_err}
+
+
+def north_star_tol(k: int, a: np.ndarray, b: np.ndarray) -> float:
+    """max|err| <= 1e-5 * sqrt(K) * max|a| * max|b| (fp32)."""
+    ma = float(np.max(np.abs(a))) if a.size else 0.0
+    mb = float(np.max(np.abs(b))) if b.size else 0.0
+    return 1e-5 * max(k, 1) ** 0.5 * ma * mb

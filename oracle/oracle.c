@@ -1,0 +1,250 @@
+/*
+ * CPU oracle for the contraction / permutation hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker (or the timed CPU
+ * baseline), never as the thing measured or shipped. The product path
+ * (liblinalg_hip.so) has no CPU fallback and never calls into this file.
+ *
+ * The reference's CPU oracle (crates/cpu, Rust) cannot be compiled here (no Rust toolchain),
+ * so this is a C restatement of the reference algorithms, each function citing what it
+ * follows. Build: gcc -O2 -ffp-contract=off (no FMA contraction, no reassociation), so every
+ * `a * b + c` below rounds twice, exactly as the reference evaluates it.
+ *
+ * Pinning (tests/test_oracle.py): the gemm functions against the known-answer vectors of
+ * crates/cpu/src/invariants.rs:137-243 (tests/golden/cpu_gemm_kats.json), closed forms
+ * (identity / permutation / integer matrices), and each other bit for bit; the gather
+ * against numpy.transpose on raw words and the complex word table of
+ * tests/permutation_test.rs:464-492; the f64 reference against numpy float64 einsum and
+ * exact integer cases.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/*
+ * CpuBackend::gemm's accumulation (crates/cpu/src/lib.rs:664-691) over a 2-D strided
+ * indexer (crates/cpu/src/lib.rs:651-656): for every (row, col) in row-major order,
+ *   acc = (beta == 0) ? +0 : beta * C[row, col]
+ *   if (alpha != 0) for inner in 0..k: acc += (alpha * A[row, inner]) * B[inner, col]
+ *   C[row, col] = acc
+ * Pointers are the views' element-offset bases; strides are in elements. The literal,
+ * single-threaded form: what crates/cpu runs.
+ */
+void oracle_gemm_seq_f32(uint64_t m, uint64_t n, uint64_t k, float alpha, float beta,
+                         const float* a, int64_t a_rs, int64_t a_cs,
+                         const float* b, int64_t b_rs, int64_t b_cs,
+                         float* c, int64_t c_rs, int64_t c_cs) {
+    for (uint64_t row = 0; row < m; ++row) {
+        for (uint64_t col = 0; col < n; ++col) {
+            float* out = c + (int64_t)row * c_rs + (int64_t)col * c_cs;
+            float acc = (beta == 0.0f) ? 0.0f : beta * *out;
+            if (alpha != 0.0f) {
+                for (uint64_t inner = 0; inner < k; ++inner) {
+                    const float t = alpha * a[(int64_t)row * a_rs + (int64_t)inner * a_cs];
+                    const float p = t * b[(int64_t)inner * b_rs + (int64_t)col * b_cs];
+                    acc = acc + p;
+                }
+            }
+            *out = acc;
+        }
+    }
+}
+
+/*
+ * The same arithmetic with the loops interchanged (inner outside, columns inside) so it
+ * vectorizes across columns and runs rows on several threads. Every output element still
+ * sees exactly the operations of oracle_gemm_seq_f32 in the same order -- (alpha*a) rounds,
+ * times b rounds, plus acc rounds, k ascending -- so the two are bit-identical (checked by
+ * the tests). B is first copied to a dense row-major K x N block (an exact copy) so the
+ * column loop is unit stride whatever B's layout.
+ *
+ * rows: optional list of `nrows` row indices to compute (NULL = all m rows, nrows ignored).
+ */
+typedef struct {
+    uint64_t n, k;
+    float alpha, beta;
+    const float* a;
+    int64_t a_rs, a_cs;
+    const float* bd; /* dense K x N */
+    float* c;
+    int64_t c_rs, c_cs;
+    const uint64_t* rows;
+    uint64_t first, last; /* range of the row list handled by this worker */
+} fast_job;
+
+#define COLS 512
+
+static void* fast_worker(void* arg) {
+    const fast_job* j = (const fast_job*)arg;
+    float acc[COLS];
+    for (uint64_t r = j->first; r < j->last; ++r) {
+        const uint64_t row = j->rows ? j->rows[r] : r;
+        for (uint64_t c0 = 0; c0 < j->n; c0 += COLS) {
+            const uint64_t cn = (j->n - c0 < COLS) ? j->n - c0 : COLS;
+            for (uint64_t col = 0; col < cn; ++col) {
+                const float cv = j->c[(int64_t)row * j->c_rs + (int64_t)(c0 + col) * j->c_cs];
+                acc[col] = (j->beta == 0.0f) ? 0.0f : j->beta * cv;
+            }
+            if (j->alpha != 0.0f) {
+                for (uint64_t inner = 0; inner < j->k; ++inner) {
+                    const float t = j->alpha * j->a[(int64_t)row * j->a_rs + (int64_t)inner * j->a_cs];
+                    const float* brow = j->bd + inner * j->n + c0;
+                    for (uint64_t col = 0; col < cn; ++col) {
+                        const float p = t * brow[col];
+                        acc[col] = acc[col] + p;
+                    }
+                }
+            }
+            for (uint64_t col = 0; col < cn; ++col) {
+                j->c[(int64_t)row * j->c_rs + (int64_t)(c0 + col) * j->c_cs] = acc[col];
+            }
+        }
+    }
+    return NULL;
+}
+
+int oracle_gemm_fast_f32(uint64_t m, uint64_t n, uint64_t k, float alpha, float beta,
+                         const float* a, int64_t a_rs, int64_t a_cs,
+                         const float* b, int64_t b_rs, int64_t b_cs,
+                         float* c, int64_t c_rs, int64_t c_cs,
+                         const uint64_t* rows, uint64_t nrows, int threads) {
+    const uint64_t count = rows ? nrows : m;
+    if (count == 0 || n == 0) return 0;
+    float* bd = NULL;
+    if (alpha != 0.0f && k > 0) {
+        bd = (float*)malloc(sizeof(float) * k * n);
+        if (!bd) return -1;
+        for (uint64_t i = 0; i < k; ++i)
+            for (uint64_t col = 0; col < n; ++col)
+                bd[i * n + col] = b[(int64_t)i * b_rs + (int64_t)col * b_cs];
+    }
+    if (threads < 1) threads = 1;
+    if ((uint64_t)threads > count) threads = (int)count;
+    fast_job jobs[256];
+    pthread_t tids[256];
+    if (threads > 256) threads = 256;
+    for (int t = 0; t < threads; ++t) {
+        fast_job* j = &jobs[t];
+        j->n = n;
+        j->k = (bd ? k : 0);
+        j->alpha = (bd ? alpha : 0.0f);
+        j->beta = beta;
+        j->a = a;
+        j->a_rs = a_rs;
+        j->a_cs = a_cs;
+        j->bd = bd;
+        j->c = c;
+        j->c_rs = c_rs;
+        j->c_cs = c_cs;
+        j->rows = rows;
+        j->first = count * (uint64_t)t / (uint64_t)threads;
+        j->last = count * (uint64_t)(t + 1) / (uint64_t)threads;
+    }
+    int rc = 0;
+    for (int t = 1; t < threads; ++t) {
+        if (pthread_create(&tids[t], NULL, fast_worker, &jobs[t]) != 0) rc = -2;
+    }
+    fast_worker(&jobs[0]);
+    for (int t = 1; t < threads; ++t) pthread_join(tids[t], NULL);
+    free(bd);
+    return rc;
+}
+
+/*
+ * gather_words (tests/permutation_test.rs:84-116): the raw 32-bit words of a view in
+ * row-major logical order; with `conj` on a complex (two-word) element the second word's
+ * sign bit is flipped. `base` is the allocation as words; offset/strides in elements of
+ * `w` words. Returns the number of words written.
+ */
+uint64_t oracle_gather_words(const uint32_t* base, uint32_t w, uint64_t offset, uint32_t rank,
+                             const uint64_t* shape, const uint64_t* strides, int conj,
+                             int complex_elem, uint32_t* out) {
+    uint64_t len = 1;
+    for (uint32_t d = 0; d < rank; ++d) len *= shape[d];
+    if (len == 0) return 0;
+    uint64_t idx[64];
+    memset(idx, 0, sizeof(idx));
+    uint64_t written = 0;
+    for (;;) {
+        uint64_t e = offset;
+        for (uint32_t d = 0; d < rank; ++d) e += idx[d] * strides[d];
+        for (uint32_t kw = 0; kw < w; ++kw) {
+            uint32_t word = base[e * w + kw];
+            if (conj && complex_elem && kw == 1) word ^= 0x80000000u;
+            out[written++] = word;
+        }
+        uint32_t d = rank;
+        for (;;) {
+            if (d == 0) return written;
+            --d;
+            if (++idx[d] < shape[d]) break;
+            idx[d] = 0;
+        }
+    }
+}
+
+/*
+ * The f64 contraction reference of tests/contraction_test.rs:200-268. For every element of
+ * C in row-major order of C's labels ("free" labels), with the contracted labels ("sum",
+ * in A's label order) running in row-major order:
+ *   exact = alpha * sum(a * b) + beta * c0     (f64; alpha = 0 skips A, B; beta = 0 skips C)
+ *   magnitude = |alpha| * sum|a * b| + |beta * c0|
+ *   index = C's element index
+ * Per-label strides are 0 for an operand that does not carry the label.
+ */
+void oracle_contract_f64(float alpha_f, float beta_f, uint32_t n_free, const uint64_t* free_ext,
+                         const int64_t* a_free, const int64_t* b_free, const int64_t* c_free,
+                         uint32_t n_sum, const uint64_t* sum_ext, const int64_t* a_sum,
+                         const int64_t* b_sum, const float* a, uint64_t a_off, const float* b,
+                         uint64_t b_off, const float* c0, uint64_t c_off, double* exact,
+                         double* magnitude, uint64_t* index) {
+    const double alpha = (double)alpha_f, beta = (double)beta_f;
+    uint64_t nf = 1, ns = 1;
+    for (uint32_t d = 0; d < n_free; ++d) nf *= free_ext[d];
+    for (uint32_t d = 0; d < n_sum; ++d) ns *= sum_ext[d];
+    uint64_t fi[64], si[64];
+    memset(fi, 0, sizeof(fi));
+    for (uint64_t i = 0; i < nf; ++i) {
+        int64_t ao = (int64_t)a_off, bo = (int64_t)b_off, co = (int64_t)c_off;
+        for (uint32_t d = 0; d < n_free; ++d) {
+            ao += (int64_t)fi[d] * a_free[d];
+            bo += (int64_t)fi[d] * b_free[d];
+            co += (int64_t)fi[d] * c_free[d];
+        }
+        double sum = 0.0, absum = 0.0;
+        if (alpha != 0.0 && ns > 0) {
+            memset(si, 0, sizeof(si));
+            for (uint64_t s = 0; s < ns; ++s) {
+                int64_t ka = 0, kb = 0;
+                for (uint32_t d = 0; d < n_sum; ++d) {
+                    ka += (int64_t)si[d] * a_sum[d];
+                    kb += (int64_t)si[d] * b_sum[d];
+                }
+                const double p = (double)a[ao + ka] * (double)b[bo + kb];
+                sum += p;
+                absum += fabs(p);
+                for (uint32_t d = n_sum; d-- > 0;) {
+                    if (++si[d] < sum_ext[d]) break;
+                    si[d] = 0;
+                }
+            }
+            sum *= alpha;
+            absum *= fabs(alpha);
+        }
+        if (beta != 0.0) {
+            const double cv = beta * (double)c0[co];
+            sum += cv;
+            absum += fabs(cv);
+        }
+        exact[i] = sum;
+        magnitude[i] = absum;
+        index[i] = (uint64_t)co;
+        for (uint32_t d = n_free; d-- > 0;) {
+            if (++fi[d] < free_ext[d]) break;
+            fi[d] = 0;
+        }
+    }
+}

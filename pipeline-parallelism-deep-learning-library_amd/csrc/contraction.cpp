@@ -1,0 +1,686 @@
+// Contraction: C = alpha * A.B + beta * C over einsum labels, and the batched GEMM form.
+//
+// Host half of the contraction hot path. Follows the reference's planner
+// (src/ops/contraction.rs) step for step where the semantics are observable:
+//   * labels -> roles batch (A,B,C) / M (A,C) / N (B,C) / K (A,B)        (:344-442)
+//   * gemm form: leading axes batch, last two M x K, K x N, M x N        (:444-494)
+//   * per group: drop extent-1 axes, merge an axis into its slower neighbour when every
+//     operand carrying it is contiguous, at most 4 strides per group     (:256-335)
+//   * destination alias analysis (exact mixed-radix decode, hash set up to 2e6 elements,
+//     conservative reject beyond)                                         (:518-662)
+//   * plan Empty / Fill / Tiled / Split / General                         (:664-867)
+// The MI355X parts are our own: the kernel geometry, the split-K sizing (targets two
+// workgroups on each of 256 CUs, independent of the device so results are reproducible
+// across boxes), the operand load modes, and 64-bit addressing (no u32 index limit).
+#include <algorithm>
+#include <cstring>
+#include <unordered_set>
+
+#include "lg_internal.h"
+
+namespace lg {
+namespace {
+
+constexpr uint64_t EXACT_LIMIT = 2000000;  // src/ops/contraction.rs:584
+constexpr uint32_t SPLIT_TARGET = 512;     // workgroups the split-K path aims for
+constexpr uint32_t SPLIT_MIN_CHUNK = 256;  // K elements per split, at least
+constexpr uint32_t SPLIT_MAX = 1024;
+
+struct Axis {
+    uint64_t extent = 1;
+    bool ha = false, hb = false, hc = false;  // operand carries the axis
+    uint64_t a = 0, b = 0, c = 0;             // its stride there
+};
+
+bool can_merge(const Axis& prev, const Axis& next) {
+    auto ok = [&](bool hp, uint64_t sp, bool hn, uint64_t sn) {
+        if (hp && hn) {
+            if (sn != 0 && next.extent > UINT64_MAX / sn) return false;
+            return sp == next.extent * sn;
+        }
+        return hp == hn;
+    };
+    return ok(prev.ha, prev.a, next.ha, next.a) && ok(prev.hb, prev.b, next.hb, next.b) &&
+           ok(prev.hc, prev.c, next.hc, next.c);
+}
+
+Axis unit_axis(uint64_t extent) {
+    Axis ax;
+    ax.extent = extent;
+    ax.ha = ax.hb = ax.hc = true;
+    return ax;
+}
+
+// merge_group (src/ops/contraction.rs:278-312).
+std::vector<Axis> merge_group(const std::vector<Axis>& axes, const char* group) {
+    for (const Axis& ax : axes) {
+        if (ax.extent == 0) return {unit_axis(0)};
+    }
+    std::vector<Axis> kept;
+    for (const Axis& ax : axes) {
+        if (ax.extent != 1) kept.push_back(ax);
+    }
+    if (kept.empty()) return {unit_axis(1)};
+    std::vector<Axis> out{kept[0]};
+    for (size_t i = 1; i < kept.size(); ++i) {
+        const Axis& ax = kept[i];
+        Axis& last = out.back();
+        if (can_merge(last, ax)) {
+            if (ax.extent != 0 && last.extent > UINT64_MAX / ax.extent) {
+                fail_invalid(std::string(group) + " extent product overflows");
+            }
+            const uint64_t extent = last.extent * ax.extent;
+            last = ax;
+            last.extent = extent;
+        } else {
+            out.push_back(ax);
+        }
+    }
+    if (out.size() > 4) {
+        fail_invalid(std::string(group) + " group has " + std::to_string(out.size()) +
+                     " strides after merging; the kernel supports 4");
+    }
+    return out;
+}
+
+struct Groups {
+    std::vector<Axis> batch, m, n, k;
+};
+
+// parse_labels (src/ops/contraction.rs:344-355). One label per byte.
+std::string parse_labels(const char* labels, size_t rank, const char* name) {
+    if (labels == nullptr) fail_invalid(std::string("null labels for ") + name);
+    std::string s(labels);
+    if (s.size() != rank) {
+        fail_invalid("label count " + std::to_string(s.size()) + " does not match rank " +
+                     std::to_string(rank));
+    }
+    for (size_t i = 0; i < s.size(); ++i) {
+        if (s.find(s[i]) != i) fail_invalid(std::string("repeated label '") + s[i] + "'");
+    }
+    return s;
+}
+
+enum class Role { Batch, M, N, K };
+
+// groups_from_labels (src/ops/contraction.rs:380-442).
+Groups groups_from_labels(const View& a, const std::string& la, const View& b,
+                          const std::string& lb, const View& c, const std::string& lc) {
+    std::string order;
+    for (const std::string* ls : {&la, &lb, &lc}) {
+        for (char ch : *ls) {
+            if (order.find(ch) == std::string::npos) order.push_back(ch);
+        }
+    }
+    struct Info {
+        char label;
+        Role role;
+        Axis axis;
+    };
+    std::vector<Info> infos;
+    for (char ch : order) {
+        const size_t pa = la.find(ch), pb = lb.find(ch), pc = lc.find(ch);
+        const bool fa = pa != std::string::npos, fb = pb != std::string::npos,
+                   fc = pc != std::string::npos;
+        Role role;
+        if (fa && fb && fc) role = Role::Batch;
+        else if (fa && !fb && fc) role = Role::M;
+        else if (!fa && fb && fc) role = Role::N;
+        else if (fa && fb && !fc) role = Role::K;
+        else if (!fa && !fb && fc) fail_invalid(std::string("label '") + ch + "' appears only in C");
+        else fail_invalid(std::string("label '") + ch + "' appears once");
+        bool have = false;
+        uint64_t extent = 1;
+        auto see = [&](bool found, const View& v, size_t p) {
+            if (!found) return;
+            if (have && extent != v.shape[p]) {
+                fail_invalid(std::string("extent mismatch for label '") + ch + "'");
+            }
+            have = true;
+            extent = v.shape[p];
+        };
+        see(fa, a, pa);
+        see(fb, b, pb);
+        see(fc, c, pc);
+        Axis ax;
+        ax.extent = extent;
+        ax.ha = fa;
+        ax.hb = fb;
+        ax.hc = fc;
+        ax.a = fa ? a.strides[pa] : 0;
+        ax.b = fb ? b.strides[pb] : 0;
+        ax.c = fc ? c.strides[pc] : 0;
+        infos.push_back({ch, role, ax});
+    }
+    auto take = [&](const std::string& labels, Role role) {
+        std::vector<Axis> out;
+        for (char ch : labels) {
+            for (const Info& info : infos) {
+                if (info.label == ch && info.role == role) out.push_back(info.axis);
+            }
+        }
+        return out;
+    };
+    Groups g;
+    g.batch = take(lc, Role::Batch);
+    g.m = take(lc, Role::M);
+    g.n = take(lc, Role::N);
+    g.k = take(la, Role::K);
+    return g;
+}
+
+// groups_from_gemm (src/ops/contraction.rs:444-494).
+Groups groups_from_gemm(const View& a, const View& b, const View& c) {
+    if (a.rank() < 2 || b.rank() < 2 || c.rank() < 2) fail_invalid("rank below 2");
+    if (a.rank() != b.rank() || b.rank() != c.rank()) fail_invalid("ranks differ");
+    const size_t r = a.rank();
+    Groups g;
+    for (size_t d = 0; d + 2 < r; ++d) {
+        if (a.shape[d] != b.shape[d] || b.shape[d] != c.shape[d]) fail_invalid("batch extents differ");
+        Axis ax;
+        ax.extent = a.shape[d];
+        ax.ha = ax.hb = ax.hc = true;
+        ax.a = a.strides[d];
+        ax.b = b.strides[d];
+        ax.c = c.strides[d];
+        g.batch.push_back(ax);
+    }
+    const uint64_t m = a.shape[r - 2], ka = a.shape[r - 1], kb = b.shape[r - 2], n = b.shape[r - 1];
+    if (m != c.shape[r - 2] || n != c.shape[r - 1] || ka != kb) fail_invalid("inner extents differ");
+    Axis am;
+    am.extent = m;
+    am.ha = am.hc = true;
+    am.a = a.strides[r - 2];
+    am.c = c.strides[r - 2];
+    Axis an;
+    an.extent = n;
+    an.hb = an.hc = true;
+    an.b = b.strides[r - 1];
+    an.c = c.strides[r - 1];
+    Axis ak;
+    ak.extent = ka;
+    ak.ha = ak.hb = true;
+    ak.a = a.strides[r - 1];
+    ak.b = b.strides[r - 2];
+    g.m = {am};
+    g.n = {an};
+    g.k = {ak};
+    return g;
+}
+
+// ---------------------------------------------------------------------------------------
+// Destination alias analysis (src/ops/contraction.rs:496-662)
+// ---------------------------------------------------------------------------------------
+bool same_buffer(const View& a, const View& b) { return a.base == b.base; }
+
+bool same_view(const View& a, const View& b) {
+    return same_buffer(a, b) && a.offset == b.offset && a.shape == b.shape && a.strides == b.strides;
+}
+
+// Extent>1 axes sorted by ascending stride when they form a unique mixed-radix address.
+bool decodable(const View& v, std::vector<std::pair<uint64_t, uint64_t>>* axes) {
+    axes->clear();
+    for (size_t d = 0; d < v.rank(); ++d) {
+        if (v.shape[d] > 1) axes->push_back({v.shape[d], v.strides[d]});
+    }
+    std::stable_sort(axes->begin(), axes->end(),
+                     [](const auto& x, const auto& y) { return x.second < y.second; });
+    for (const auto& ax : *axes) {
+        if (ax.second == 0) return false;
+    }
+    for (size_t i = 1; i < axes->size(); ++i) {
+        const uint64_t extent = (*axes)[i - 1].first, stride = (*axes)[i - 1].second;
+        if (extent != 0 && stride > UINT64_MAX / extent) return false;
+        if ((*axes)[i].second < stride * extent) return false;
+    }
+    return true;
+}
+
+bool contains(const View& v, uint64_t elem, const std::vector<std::pair<uint64_t, uint64_t>>& asc) {
+    if (elem < v.offset) return false;
+    uint64_t rem = elem - v.offset;
+    for (size_t i = asc.size(); i-- > 0;) {
+        const uint64_t coord = rem / asc[i].second;
+        if (coord >= asc[i].first) return false;
+        rem -= coord * asc[i].second;
+    }
+    return rem == 0;
+}
+
+template <typename F>
+void for_each_index(const View& v, F&& visit) {
+    if (v.is_empty()) return;
+    const size_t rank = v.rank();
+    if (rank == 0) {
+        visit(v.offset);
+        return;
+    }
+    std::vector<uint64_t> idx(rank, 0);
+    for (;;) {
+        uint64_t e = v.offset;
+        for (size_t d = 0; d < rank; ++d) e += idx[d] * v.strides[d];
+        if (!visit(e)) return;
+        size_t axis = rank - 1;
+        for (;;) {
+            if (++idx[axis] < v.shape[axis]) break;
+            idx[axis] = 0;
+            if (axis == 0) return;
+            --axis;
+        }
+    }
+}
+
+bool shares(const View& a, const View& b) {
+    if (!same_buffer(a, b)) return false;
+    uint64_t a0, a1, b0, b1;
+    if (!element_range(a, &a0, &a1) || !element_range(b, &b0, &b1)) return false;
+    if (a0 >= b1 || b0 >= a1) return false;
+    const bool a_small = a.len() <= b.len();
+    const View& small = a_small ? a : b;
+    const View& large = a_small ? b : a;
+    std::vector<std::pair<uint64_t, uint64_t>> axes;
+    bool hit = false;
+    if (decodable(large, &axes)) {
+        for_each_index(small, [&](uint64_t e) {
+            hit = contains(large, e, axes);
+            return !hit;
+        });
+        return hit;
+    }
+    // Unusual strides (or a stride of 0): exact for modest views, otherwise report overlap
+    // rather than launch a kernel that would race.
+    if (large.len() > EXACT_LIMIT) return true;
+    std::unordered_set<uint64_t> seen;
+    seen.reserve(large.len());
+    for_each_index(large, [&](uint64_t e) {
+        seen.insert(e);
+        return true;
+    });
+    for_each_index(small, [&](uint64_t e) {
+        hit = seen.count(e) != 0;
+        return !hit;
+    });
+    return hit;
+}
+
+bool self_overlaps(const View& v) {
+    std::vector<std::pair<uint64_t, uint64_t>> axes;
+    if (v.len() <= 1 || decodable(v, &axes)) return false;
+    if (v.len() > EXACT_LIMIT) return true;
+    std::unordered_set<uint64_t> seen;
+    seen.reserve(v.len());
+    bool overlap = false;
+    for_each_index(v, [&](uint64_t e) {
+        if (!seen.insert(e).second) overlap = true;
+        return !overlap;
+    });
+    return overlap;
+}
+
+void check_destination_alias(const View& a, const View& b, const View& c, uint64_t m, uint64_t n,
+                             uint64_t k, bool reads_inputs) {
+    if (self_overlaps(c)) fail_overlap("C writes the same element more than once");
+    if (!reads_inputs) return;
+    // In-place scale: C is A (or B) and every other extent is 1, so each output reads only
+    // its own previous value. A and B may still alias each other.
+    const bool inplace_a = k == 1 && n == 1 && same_view(c, a) && !shares(c, b);
+    const bool inplace_b = k == 1 && m == 1 && same_view(c, b) && !shares(c, a);
+    if (!inplace_a && (same_view(c, a) || shares(c, a))) fail_overlap("C overlaps A");
+    if (!inplace_b && (same_view(c, b) || shares(c, b))) fail_overlap("C overlaps B");
+}
+
+// ---------------------------------------------------------------------------------------
+// Planning
+// ---------------------------------------------------------------------------------------
+struct Merged {
+    std::vector<Axis> batch, m, n, k;
+    uint64_t batch_n = 1, m_n = 1, n_n = 1, k_n = 1;
+};
+
+uint64_t product(const std::vector<Axis>& axes) {
+    uint64_t acc = 1;
+    for (const Axis& ax : axes) {
+        if (ax.extent != 0 && acc > UINT64_MAX / ax.extent) fail_invalid("dimension product overflows");
+        acc *= ax.extent;
+    }
+    return acc;
+}
+
+Merged merge_all(const Groups& g) {
+    Merged r;
+    r.batch = merge_group(g.batch, "batch");
+    r.m = merge_group(g.m, "M");
+    r.n = merge_group(g.n, "N");
+    r.k = merge_group(g.k, "K");
+    r.batch_n = product(r.batch);
+    r.m_n = product(r.m);
+    r.n_n = product(r.n);
+    r.k_n = product(r.k);
+    return r;
+}
+
+uint32_t fit32(uint64_t x, const char* what) {
+    if (x > 0x7fffffffull) {
+        fail_invalid(std::string(what) + " " + std::to_string(x) +
+                     " exceeds the kernels' 31-bit extent limit");
+    }
+    return static_cast<uint32_t>(x);
+}
+
+int64_t sfit(uint64_t x, const char* what) {
+    if (x > static_cast<uint64_t>(INT64_MAX)) fail_invalid(std::string(what) + " too large");
+    return static_cast<int64_t>(x);
+}
+
+Axes4 pack(const std::vector<Axis>& axes, char which) {
+    Axes4 out;
+    for (int i = 0; i < 4; ++i) {
+        out.ext[i] = 1;
+        out.stride[i] = 0;
+    }
+    const size_t n = axes.size();
+    for (size_t i = 0; i < n; ++i) {
+        const size_t slot = 4 - n + i;
+        out.ext[slot] = fit32(axes[i].extent, "extent");
+        const uint64_t s = which == 'a' ? axes[i].a : which == 'b' ? axes[i].b : axes[i].c;
+        out.stride[slot] = sfit(s, "stride");
+    }
+    return out;
+}
+
+struct Plan {
+    lg_contract_plan info{};
+    GemmArgs gemm{};
+    ReduceArgs reduce{};
+    GeneralArgs general{};
+    FillArgs fill{};
+};
+
+// (splits, k_chunk): one split when the output already fills the chip or K is short.
+void split_shape(uint64_t tiles, uint32_t k, uint32_t* splits, uint32_t* chunk) {
+    *splits = 1;
+    *chunk = k;
+    if (tiles >= SPLIT_TARGET / 2 || k < 2 * SPLIT_MIN_CHUNK) return;
+    const uint64_t want = (SPLIT_TARGET + tiles - 1) / tiles;
+    const uint64_t by_k = k / SPLIT_MIN_CHUNK;
+    const uint64_t rough = std::max<uint64_t>(1, std::min<uint64_t>({want, by_k, SPLIT_MAX}));
+    uint64_t c = (k + rough - 1) / rough;
+    c = (c + GEMM_BK - 1) / GEMM_BK * GEMM_BK;
+    if (c == 0 || c >= k) return;
+    *chunk = static_cast<uint32_t>(c);
+    *splits = static_cast<uint32_t>((k + c - 1) / c);
+}
+
+// 128-bit loads need the view's first element 16-byte aligned (allocation base included) and
+// every other stride a multiple of four elements.
+int load_mode(uintptr_t base, uint64_t off, uint64_t sb, uint64_t srow, uint64_t sk) {
+    auto al = [](uint64_t x) { return x % 4 == 0; };
+    const bool start = (base + off * sizeof(float)) % 16 == 0;
+    if (sk == 1 && start && al(srow) && al(sb)) return LOAD_K;
+    if (srow == 1 && start && al(sk) && al(sb)) return LOAD_MN;
+    return LOAD_S;
+}
+
+Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, float alpha,
+                 float beta) {
+    Plan p;
+    lg_contract_plan& info = p.info;
+    info.batch = mg.batch_n;
+    info.m = mg.m_n;
+    info.n = mg.n_n;
+    info.k = mg.k_n;
+    info.splits = 1;
+    info.k_chunk = mg.k_n;
+    info.groups = static_cast<uint32_t>(
+        std::max({mg.batch.size(), mg.m.size(), mg.n.size(), mg.k.size()}));
+    if (mg.m_n == 0 || mg.n_n == 0 || mg.batch_n == 0) {
+        info.kind = LG_PLAN_EMPTY;
+        return p;
+    }
+    const bool reads_inputs = alpha != 0.0f && mg.k_n != 0;
+    check_destination_alias(a, b, c, mg.m_n, mg.n_n, mg.k_n, reads_inputs);
+    float* cptr = reinterpret_cast<float*>(c.base) + c.offset;
+    if (!reads_inputs) {
+        info.kind = beta == 0.0f ? LG_PLAN_ZERO : LG_PLAN_SCALE;
+        FillArgs& f = p.fill;
+        f.c = cptr;
+        f.count = mg.batch_n * mg.m_n * mg.n_n;
+        f.m = fit32(mg.m_n, "M");
+        f.n = fit32(mg.n_n, "N");
+        f.batch = fit32(mg.batch_n, "batch");
+        f.beta = beta;
+        f.c_batch = pack(mg.batch, 'c');
+        f.c_m = pack(mg.m, 'c');
+        f.c_n = pack(mg.n, 'c');
+        info.workgroups = (f.count + 255) / 256;
+        return p;
+    }
+    const uint32_t m = fit32(mg.m_n, "M"), n = fit32(mg.n_n, "N"), k = fit32(mg.k_n, "K"),
+                   batch = fit32(mg.batch_n, "batch");
+    const float* aptr = reinterpret_cast<const float*>(a.base) + a.offset;
+    const float* bptr = reinterpret_cast<const float*>(b.base) + b.offset;
+    const bool single = mg.batch.size() == 1 && mg.m.size() == 1 && mg.n.size() == 1 &&
+                        mg.k.size() == 1;
+    if (!single) {
+        info.kind = LG_PLAN_GENERAL;
+        GeneralArgs& g = p.general;
+        g.a = aptr;
+        g.b = bptr;
+        g.c = cptr;
+        g.m = m;
+        g.n = n;
+        g.k = k;
+        g.batch = batch;
+        g.alpha = alpha;
+        g.beta = beta;
+        g.a_batch = pack(mg.batch, 'a');
+        g.a_m = pack(mg.m, 'a');
+        g.a_k = pack(mg.k, 'a');
+        g.b_batch = pack(mg.batch, 'b');
+        g.b_n = pack(mg.n, 'b');
+        g.b_k = pack(mg.k, 'b');
+        g.c_batch = pack(mg.batch, 'c');
+        g.c_m = pack(mg.m, 'c');
+        g.c_n = pack(mg.n, 'c');
+        info.workgroups = (mg.batch_n * mg.m_n * mg.n_n + 255) / 256;
+        return p;
+    }
+    const Axis &ab = mg.batch[0], &am = mg.m[0], &an = mg.n[0], &ak = mg.k[0];
+    GemmArgs& t = p.gemm;
+    t.a = aptr;
+    t.b = bptr;
+    t.c = cptr;
+    t.partial = nullptr;
+    t.a_sb = sfit(ab.a, "A batch stride");
+    t.a_sm = sfit(am.a, "A M stride");
+    t.a_sk = sfit(ak.a, "A K stride");
+    t.b_sb = sfit(ab.b, "B batch stride");
+    t.b_sn = sfit(an.b, "B N stride");
+    t.b_sk = sfit(ak.b, "B K stride");
+    t.c_sb = sfit(ab.c, "C batch stride");
+    t.c_sm = sfit(am.c, "C M stride");
+    t.c_sn = sfit(an.c, "C N stride");
+    t.m = m;
+    t.n = n;
+    t.k = k;
+    t.batch = batch;
+    t.alpha = alpha;
+    t.beta = beta;
+    t.tiles_m = (m + GEMM_BM - 1) / GEMM_BM;
+    t.tiles_n = (n + GEMM_BN - 1) / GEMM_BN;
+    const int a_mode = load_mode(a.base, a.offset, ab.a, am.a, ak.a);
+    const int b_mode = load_mode(b.base, b.offset, ab.b, an.b, ak.b);
+    info.a_mode = static_cast<uint32_t>(a_mode);
+    info.b_mode = static_cast<uint32_t>(b_mode);
+    const uint64_t tiles = static_cast<uint64_t>(t.tiles_m) * t.tiles_n * batch;
+    uint32_t splits = 1, chunk = k;
+    split_shape(tiles, k, &splits, &chunk);
+    if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
+    t.splits = splits;
+    t.k_chunk = chunk;
+    info.splits = splits;
+    info.k_chunk = chunk;
+    info.workgroups = gemm_workgroups(m, n, batch, splits);
+    if (splits == 1) {
+        info.kind = LG_PLAN_TILED;
+        return p;
+    }
+    info.kind = LG_PLAN_SPLIT;
+    info.scratch_bytes = static_cast<uint64_t>(splits) * batch * m * n * sizeof(float);
+    ReduceArgs& r = p.reduce;
+    r.c = cptr;
+    r.c_sb = t.c_sb;
+    r.c_sm = t.c_sm;
+    r.c_sn = t.c_sn;
+    r.m = m;
+    r.n = n;
+    r.batch = batch;
+    r.splits = splits;
+    r.alpha = alpha;
+    r.beta = beta;
+    return p;
+}
+
+void prepare_views(const View& a, const View& b, const View& c) {
+    validate(a, 4);
+    validate(b, 4);
+    validate(c, 4);
+}
+
+Plan plan_contract(float alpha, const lg_view* a_c, const char* la, const lg_view* b_c,
+                   const char* lb, float beta, const lg_view* c_c, const char* lc, View* a,
+                   View* b, View* c) {
+    *a = view_from_c(a_c, "A");
+    *b = view_from_c(b_c, "B");
+    *c = view_from_c(c_c, "C");
+    prepare_views(*a, *b, *c);
+    const std::string sa = parse_labels(la, a->rank(), "A");
+    const std::string sb = parse_labels(lb, b->rank(), "B");
+    const std::string sc = parse_labels(lc, c->rank(), "C");
+    return plan_merged(*a, *b, *c, merge_all(groups_from_labels(*a, sa, *b, sb, *c, sc)), alpha,
+                       beta);
+}
+
+Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, const lg_view* c_c,
+               View* a, View* b, View* c) {
+    *a = view_from_c(a_c, "A");
+    *b = view_from_c(b_c, "B");
+    *c = view_from_c(c_c, "C");
+    prepare_views(*a, *b, *c);
+    return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta);
+}
+
+void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
+    switch (p.info.kind) {
+        case LG_PLAN_EMPTY:
+            return;
+        case LG_PLAN_ZERO:
+        case LG_PLAN_SCALE:
+            launch_fill(ctx, s, p.fill);
+            return;
+        case LG_PLAN_GENERAL:
+            launch_general(ctx, s, p.general);
+            return;
+        case LG_PLAN_TILED:
+            launch_gemm(ctx, s, p.gemm, static_cast<int>(p.info.a_mode),
+                        static_cast<int>(p.info.b_mode));
+            return;
+        case LG_PLAN_SPLIT: {
+            // Stream-ordered scratch: freed after the reduction on the same stream, so it
+            // outlives the enqueued work without host-side tracking.
+            void* partial = nullptr;
+            check_hip(hipMallocAsync(&partial, p.info.scratch_bytes, s), "hipMallocAsync");
+            p.gemm.partial = static_cast<float*>(partial);
+            p.reduce.partial = static_cast<const float*>(partial);
+            launch_gemm(ctx, s, p.gemm, static_cast<int>(p.info.a_mode),
+                        static_cast<int>(p.info.b_mode));
+            launch_reduce(ctx, s, p.reduce);
+            check_hip(hipFreeAsync(partial, s), "hipFreeAsync");
+            return;
+        }
+    }
+}
+
+void run(lg_ctx* ctx, void* stream, Plan plan, bool wait) {
+    set_device(ctx);
+    hipStream_t s = pick_stream(ctx, stream);
+    execute(ctx, s, plan);
+    if (wait) check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+}  // namespace
+}  // namespace lg
+
+using namespace lg;
+
+extern "C" {
+
+lg_status lg_encode_contract_f32(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                 const char* a_labels, const lg_view* b, const char* b_labels,
+                                 float beta, const lg_view* c, const char* c_labels) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, stream,
+            plan_contract(alpha, a, a_labels, b, b_labels, beta, c, c_labels, &va, &vb, &vc), false);
+    });
+}
+
+lg_status lg_contract_f32(lg_ctx* ctx, float alpha, const lg_view* a, const char* a_labels,
+                          const lg_view* b, const char* b_labels, float beta, const lg_view* c,
+                          const char* c_labels) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, nullptr,
+            plan_contract(alpha, a, a_labels, b, b_labels, beta, c, c_labels, &va, &vb, &vc), true);
+    });
+}
+
+lg_status lg_encode_gemm_f32(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                             const lg_view* b, float beta, const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, stream, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc), false);
+    });
+}
+
+lg_status lg_gemm_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b, float beta,
+                      const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, nullptr, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc), true);
+    });
+}
+
+lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b,
+                             float beta, const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, nullptr, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc), false);
+    });
+}
+
+lg_status lg_plan_contract_f32(float alpha, const lg_view* a, const char* a_labels,
+                               const lg_view* b, const char* b_labels, float beta,
+                               const lg_view* c, const char* c_labels, lg_contract_plan* out) {
+    return guarded([&] {
+        if (out == nullptr) fail_invalid("null output plan");
+        View va, vb, vc;
+        *out = plan_contract(alpha, a, a_labels, b, b_labels, beta, c, c_labels, &va, &vb, &vc).info;
+    });
+}
+
+lg_status lg_plan_gemm_f32(float alpha, const lg_view* a, const lg_view* b, float beta,
+                           const lg_view* c, lg_contract_plan* out) {
+    return guarded([&] {
+        if (out == nullptr) fail_invalid("null output plan");
+        View va, vb, vc;
+        *out = plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc).info;
+    });
+}
+
+}  // extern "C"

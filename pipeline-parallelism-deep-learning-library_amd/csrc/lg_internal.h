@@ -1,0 +1,199 @@
+// Internal interfaces between the host planner (C++) and the gfx950 kernels (HIP).
+//
+// Kernel argument structs are passed by value. All element offsets and strides are 64-bit
+// (one MI355X holds 288 GB, so views far past 2^32 elements are legal); extents handed to
+// a kernel are 32-bit and the planner proves they fit.
+#pragma once
+
+#include <atomic>
+#include <cstdint>
+#include <new>
+#include <string>
+#include <vector>
+
+#include <hip/hip_runtime.h>
+
+#include "linalg_hip.h"
+
+namespace lg {
+
+// ---------------------------------------------------------------------------------------
+// Errors: thrown inside the library, turned into lg_status at the C boundary.
+// ---------------------------------------------------------------------------------------
+struct Failure {
+    lg_status status;
+    std::string message;
+};
+[[noreturn]] void fail_invalid(const std::string& msg);
+[[noreturn]] void fail_overlap(const std::string& msg);
+[[noreturn]] void fail_kernel(const std::string& msg);
+[[noreturn]] void fail_no_device(const std::string& msg);
+void check_hip(hipError_t err, const char* what);
+
+// ---------------------------------------------------------------------------------------
+// Host copy of an lg_view (TensorView, src/abi.rs:64-76).
+// ---------------------------------------------------------------------------------------
+struct View {
+    uintptr_t base = 0;
+    uint64_t bytes = 0;
+    uint64_t offset = 0;
+    std::vector<uint64_t> shape;
+    std::vector<uint64_t> strides;
+
+    size_t rank() const { return shape.size(); }
+    bool is_empty() const;
+    // Product of extents; fails InvalidArgument on overflow.
+    uint64_t len() const;
+};
+
+View view_from_c(const lg_view* v, const char* name);
+void view_to_c(const View& v, lg_view* out);
+// TensorView::validate (src/abi.rs:140-177).
+void validate(const View& v, uint32_t elem_bytes);
+// One past the last reachable element, or false for an empty view (element_range).
+bool element_range(const View& v, uint64_t* first, uint64_t* end_exclusive);
+// TensorView::may_overlap (src/abi.rs:193-204).
+bool may_overlap(const View& a, uint32_t ea, const View& b, uint32_t eb);
+std::vector<uint64_t> row_major_strides(const std::vector<uint64_t>& shape);
+std::string fmt_vec(const std::vector<uint64_t>& v);
+
+// ---------------------------------------------------------------------------------------
+// Context: one device, one default stream, a launch log.
+// ---------------------------------------------------------------------------------------
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::atomic<uint64_t> launches{0};
+    std::atomic<const char*> names[256];
+};
+void note_launch(Context* ctx, const char* name);
+void set_last_error(const std::string& msg);
+void clear_last_error();
+
+// Runs `body`, translating failures into a status and the thread's last-error message.
+template <typename F>
+lg_status guarded(F&& body) {
+    try {
+        body();
+        clear_last_error();
+        return LG_OK;
+    } catch (const Failure& f) {
+        set_last_error(f.message);
+        return f.status;
+    } catch (const std::bad_alloc&) {
+        set_last_error("host allocation failed");
+        return LG_KERNEL;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Contraction kernels
+// ---------------------------------------------------------------------------------------
+enum LoadMode : int { LOAD_K = 0, LOAD_MN = 1, LOAD_S = 2 };
+
+// Tile geometry of the MFMA GEMM kernel.
+constexpr uint32_t GEMM_BM = 128;
+constexpr uint32_t GEMM_BN = 128;
+constexpr uint32_t GEMM_BK = 32;
+constexpr uint32_t GEMM_THREADS = 256;
+
+struct GemmArgs {
+    const float* a;  // element pointer of A's view offset
+    const float* b;
+    float* c;
+    float* partial;  // split-K partials [batch][splits][m][n], or null
+    int64_t a_sb, a_sm, a_sk;
+    int64_t b_sb, b_sn, b_sk;
+    int64_t c_sb, c_sm, c_sn;
+    uint32_t m, n, k, batch;
+    uint32_t k_chunk, splits;
+    uint32_t tiles_m, tiles_n;
+    float alpha, beta;
+};
+
+struct ReduceArgs {
+    const float* partial;
+    float* c;
+    int64_t c_sb, c_sm, c_sn;
+    uint32_t m, n, batch, splits;
+    float alpha, beta;
+};
+
+// Right-aligned mixed radix of up to 4 axes (slot 3 fastest); unused slots have extent 1.
+struct Axes4 {
+    uint32_t ext[4];
+    int64_t stride[4];
+};
+
+struct GeneralArgs {
+    const float* a;
+    const float* b;
+    float* c;
+    uint32_t m, n, k, batch;
+    float alpha, beta;
+    Axes4 a_batch, a_m, a_k, b_batch, b_n, b_k, c_batch, c_m, c_n;
+};
+
+struct FillArgs {
+    float* c;
+    uint64_t count;
+    uint32_t m, n, batch;
+    float beta;
+    Axes4 c_batch, c_m, c_n;
+};
+
+void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode);
+void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args);
+void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args);
+void launch_fill(Context* ctx, hipStream_t s, const FillArgs& args);
+uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits);
+
+// ---------------------------------------------------------------------------------------
+// Permutation kernels
+// ---------------------------------------------------------------------------------------
+constexpr uint32_t PERM_MAX_RANK = 8;  // MAX_RANK, src/ops/permutation.rs:14-16
+constexpr uint32_t PERM_TILE = 64;     // edge of the LDS transpose tile, in elements
+constexpr uint32_t PERM_THREADS = 256;
+
+struct PermTileArgs {
+    const void* src;  // allocation bases
+    void* dst;
+    uint64_t src_offset, dst_offset;  // elements
+    uint32_t ext_a, ext_b;            // a: source unit-stride axis; b: destination unit-stride axis
+    int64_t src_sb, dst_sa;           // source stride of b, destination stride of a
+    uint32_t outer_rank;
+    uint32_t tiles_a, tiles_b;
+    uint64_t total_tiles;
+    uint32_t outer_shape[PERM_MAX_RANK];
+    int64_t outer_src[PERM_MAX_RANK];
+    int64_t outer_dst[PERM_MAX_RANK];
+};
+
+struct PermCopyArgs {
+    const void* src;
+    void* dst;
+    uint64_t src_offset, dst_offset, count;
+    uint32_t rank;
+    uint32_t contiguous;  // rank 1, unit stride, aligned: straight vector copy
+    uint32_t vec_dst;     // destination offset aligned for 128-bit stores
+    uint64_t shape[PERM_MAX_RANK];
+    int64_t strides[PERM_MAX_RANK];
+};
+
+// words: 1 (4-byte elements) or 2 (8-byte complex); conj flips the imaginary sign bit.
+void launch_perm_tile(Context* ctx, hipStream_t s, const PermTileArgs& args, int words, bool conj,
+                      bool vec);
+void launch_perm_copy(Context* ctx, hipStream_t s, const PermCopyArgs& args, int words, bool conj);
+uint64_t perm_copy_workgroups(uint64_t count, int words);
+uint64_t perm_tile_workgroups(uint64_t total_tiles);
+
+}  // namespace lg
+
+struct lg_ctx : lg::Context {};
+
+namespace lg {
+void set_device(const lg_ctx* ctx);
+inline hipStream_t pick_stream(const lg_ctx* ctx, void* stream) {
+    return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+}
+}  // namespace lg

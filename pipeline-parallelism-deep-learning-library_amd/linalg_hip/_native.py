@@ -1,0 +1,100 @@
+"""ctypes binding of include/linalg_hip.h (the C ABI of liblinalg_hip.so).
+
+Loading fails loudly when the library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("LINALG_HIP_LIB", PACKAGE_DIR / "liblinalg_hip.so"))
+
+LG_MAX_RANK = 16
+LG_ALLOC_GRANULE = 16384
+
+LG_OK, LG_NO_DEVICE, LG_INVALID_ARGUMENT, LG_OVERLAP, LG_KERNEL = range(5)
+LG_ELEM_F32, LG_ELEM_U32, LG_ELEM_I32, LG_ELEM_C32 = range(4)
+PLAN_KINDS = ["empty", "zero", "scale", "tiled", "split", "general"]
+LOAD_MODES = ["k", "mn", "strided"]
+PERMUTE_KINDS = ["empty", "copy", "tile"]
+
+u32, u64, i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32
+vp, cp = ctypes.c_void_p, ctypes.c_char_p
+
+
+class lg_view(ctypes.Structure):
+    _fields_ = [("base", vp), ("bytes", u64), ("offset", u64), ("rank", u32), ("nstrides", u32),
+                ("shape", u64 * LG_MAX_RANK), ("strides", u64 * LG_MAX_RANK)]
+
+
+class lg_contract_plan(ctypes.Structure):
+    _fields_ = [("kind", u32), ("a_mode", u32), ("b_mode", u32), ("groups", u32),
+                ("batch", u64), ("m", u64), ("n", u64), ("k", u64), ("splits", u64),
+                ("k_chunk", u64), ("workgroups", u64), ("scratch_bytes", u64)]
+
+
+class lg_permute_plan(ctypes.Structure):
+    _fields_ = [("kind", u32), ("rank", u32), ("axis_a", u32), ("axis_b", u32), ("vector", u32),
+                ("conj", u32), ("shape", u64 * 8), ("strides", u64 * 8), ("workgroups", u64)]
+
+
+VP = ctypes.POINTER(lg_view)
+F = ctypes.c_float
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES = {
+    "lg_last_error": (cp, []),
+    "lg_ctx_create": (i32, [i32, ctypes.POINTER(vp)]),
+    "lg_ctx_destroy": (None, [vp]),
+    "lg_ctx_stream": (vp, [vp]),
+    "lg_ctx_sync": (i32, [vp]),
+    "lg_stream_sync": (i32, [vp, vp]),
+    "lg_stream_create": (i32, [vp, ctypes.POINTER(vp)]),
+    "lg_stream_destroy": (i32, [vp, vp]),
+    "lg_alloc": (i32, [vp, u64, u64, ctypes.POINTER(vp), ctypes.POINTER(u64)]),
+    "lg_free": (i32, [vp, vp]),
+    "lg_upload": (i32, [vp, vp, u64, vp, u64]),
+    "lg_download": (i32, [vp, vp, u64, vp, u64]),
+    "lg_view_validate": (i32, [VP, u32]),
+    "lg_view_may_overlap": (i32, [VP, u32, VP, u32]),
+    "lg_permute_view": (i32, [VP, ctypes.POINTER(u64), u32, VP]),
+    "lg_encode_materialize": (i32, [vp, vp, i32, VP, VP]),
+    "lg_materialize": (i32, [vp, i32, VP, VP]),
+    "lg_encode_conjugate": (i32, [vp, vp, i32, VP, VP]),
+    "lg_conjugate": (i32, [vp, i32, VP, VP]),
+    "lg_encode_adjoint": (i32, [vp, vp, i32, VP, VP]),
+    "lg_adjoint": (i32, [vp, i32, VP, VP]),
+    "lg_encode_contract_f32": (i32, [vp, vp, F, VP, cp, VP, cp, F, VP, cp]),
+    "lg_contract_f32": (i32, [vp, F, VP, cp, VP, cp, F, VP, cp]),
+    "lg_encode_gemm_f32": (i32, [vp, vp, F, VP, VP, F, VP]),
+    "lg_gemm_f32": (i32, [vp, F, VP, VP, F, VP]),
+    "lg_gemm_nowait_f32": (i32, [vp, F, VP, VP, F, VP]),
+    "lg_plan_contract_f32": (i32, [F, VP, cp, VP, cp, F, VP, cp,
+                                   ctypes.POINTER(lg_contract_plan)]),
+    "lg_plan_gemm_f32": (i32, [F, VP, VP, F, VP, ctypes.POINTER(lg_contract_plan)]),
+    "lg_plan_permute": (i32, [u32, i32, VP, VP, ctypes.POINTER(lg_permute_plan)]),
+    "lg_debug_launch_count": (u64, [vp]),
+    "lg_debug_launch_name": (cp, [vp, u64]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded liblinalg_hip.so. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with "
+                f"`python pipeline-parallelism-deep-learning-library_amd/build.py` "
+                f"(there is no CPU fallback)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib

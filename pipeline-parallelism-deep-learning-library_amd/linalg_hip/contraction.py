@@ -1,0 +1,98 @@
+"""Tensor contraction: C = alpha*A.B + beta*C, batched GEMM, contraction over shared axes.
+
+Mirrors `linalg::ops::contraction` (src/ops/contraction.rs:1024-1130): `contract`,
+`encode_contract`, `gemm`, `encode_gemm`, `gemm_nowait`, with operands given as
+`(view, labels)` pairs like the reference's `Operand`. Errors raise InvalidArgument or
+Overlap and launch nothing. f32 only.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _native as N
+from .abi import Context, InvalidArgument, Stream, TensorView, check
+
+
+def _f32(*views: TensorView) -> None:
+    for v in views:
+        if v.dtype != "f32":
+            raise InvalidArgument(f"contraction supports f32 views, got {v.dtype}")
+
+
+def _labels(s: str) -> bytes:
+    b = s.encode()
+    if len(b) != len(s):
+        raise InvalidArgument("labels must be ASCII, one byte per axis")
+    return b
+
+
+def encode_contract(ctx: Context, stream: Stream, alpha: float, a, b, beta: float, c) -> None:
+    """Enqueues C = alpha*A.B + beta*C on `stream` (encode_contract, :1036-1048)."""
+    (av, la), (bv, lb), (cv, lc) = a, b, c
+    _f32(av, bv, cv)
+    check(N.lib().lg_encode_contract_f32(ctx.handle, stream.handle if stream else None, alpha,
+                                         ctypes.byref(av.to_c()), _labels(la),
+                                         ctypes.byref(bv.to_c()), _labels(lb), beta,
+                                         ctypes.byref(cv.to_c()), _labels(lc)))
+
+
+def contract(ctx: Context, alpha: float, a, b, beta: float, c) -> None:
+    """Synchronous encode_contract (contract, :1053-1064)."""
+    (av, la), (bv, lb), (cv, lc) = a, b, c
+    _f32(av, bv, cv)
+    check(N.lib().lg_contract_f32(ctx.handle, alpha, ctypes.byref(av.to_c()), _labels(la),
+                                  ctypes.byref(bv.to_c()), _labels(lb), beta,
+                                  ctypes.byref(cv.to_c()), _labels(lc)))
+
+
+def encode_gemm(ctx: Context, stream: Stream, alpha: float, a: TensorView, b: TensorView,
+                beta: float, c: TensorView) -> None:
+    """Enqueues the batched matrix product (encode_gemm, :1080-1090)."""
+    _f32(a, b, c)
+    check(N.lib().lg_encode_gemm_f32(ctx.handle, stream.handle if stream else None, alpha,
+                                     ctypes.byref(a.to_c()), ctypes.byref(b.to_c()), beta,
+                                     ctypes.byref(c.to_c())))
+
+
+def gemm(ctx: Context, alpha: float, a: TensorView, b: TensorView, beta: float,
+         c: TensorView) -> None:
+    """Synchronous encode_gemm (gemm, :1092-1103)."""
+    _f32(a, b, c)
+    check(N.lib().lg_gemm_f32(ctx.handle, alpha, ctypes.byref(a.to_c()), ctypes.byref(b.to_c()),
+                              beta, ctypes.byref(c.to_c())))
+
+
+def gemm_nowait(ctx: Context, alpha: float, a: TensorView, b: TensorView, beta: float,
+                c: TensorView) -> Stream:
+    """Enqueues on the context stream without waiting and returns it (gemm_nowait, :1105-1130)."""
+    _f32(a, b, c)
+    check(N.lib().lg_gemm_nowait_f32(ctx.handle, alpha, ctypes.byref(a.to_c()),
+                                     ctypes.byref(b.to_c()), beta, ctypes.byref(c.to_c())))
+    return ctx.queue
+
+
+def _plan_dict(p: N.lg_contract_plan) -> dict:
+    return {"kind": N.PLAN_KINDS[p.kind], "a_mode": N.LOAD_MODES[p.a_mode],
+            "b_mode": N.LOAD_MODES[p.b_mode], "groups": p.groups, "batch": p.batch, "m": p.m,
+            "n": p.n, "k": p.k, "splits": p.splits, "k_chunk": p.k_chunk,
+            "workgroups": p.workgroups, "scratch_bytes": p.scratch_bytes}
+
+
+def plan_contract(alpha: float, a, b, beta: float, c) -> dict:
+    """The plan `contract` would launch (host only, no device work)."""
+    (av, la), (bv, lb), (cv, lc) = a, b, c
+    _f32(av, bv, cv)
+    out = N.lg_contract_plan()
+    check(N.lib().lg_plan_contract_f32(alpha, ctypes.byref(av.to_c()), _labels(la),
+                                       ctypes.byref(bv.to_c()), _labels(lb), beta,
+                                       ctypes.byref(cv.to_c()), _labels(lc), ctypes.byref(out)))
+    return _plan_dict(out)
+
+
+def plan_gemm(alpha: float, a: TensorView, b: TensorView, beta: float, c: TensorView) -> dict:
+    """The plan `gemm` would launch (host only, no device work)."""
+    _f32(a, b, c)
+    out = N.lg_contract_plan()
+    check(N.lib().lg_plan_gemm_f32(alpha, ctypes.byref(a.to_c()), ctypes.byref(b.to_c()), beta,
+                                   ctypes.byref(c.to_c()), ctypes.byref(out)))
+    return _plan_dict(out)

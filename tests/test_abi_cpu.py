@@ -1,0 +1,347 @@
+"""Host-side tests of the C ABI and the planner (CPU only, no device work).
+
+The library is loaded and every symbol include/linalg_hip.h declares must be exported.
+View validation, permute_view, the contraction and permutation planners, and their error
+precedence are exercised through the plan-inspection entry points, which run the exact
+validation and planning of the launching entry points. Buffers here are fake device
+addresses that the planner never dereferences.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+
+import numpy as np
+import pytest
+
+import linalg_hip as L
+from helpers import GOLDEN, Layout
+from linalg_hip import _native as N
+from linalg_hip import contraction as C
+from linalg_hip import permutation as P
+
+HEADER = (GOLDEN.parent.parent / "include" / "linalg_hip.h").read_text()
+PKATS = json.loads((GOLDEN / "permutation_kats.json").read_text())
+
+_next_base = [0x10000000]
+
+
+def fake(nbytes: int) -> L.Buffer:
+    """A fake allocation at a distinct 16 KiB-aligned address (never dereferenced)."""
+    base = _next_base[0]
+    _next_base[0] += ((nbytes + 16383) // 16384 + 1) * 16384
+    return L.Buffer(None, base, max(16384, (nbytes + 16383) // 16384 * 16384))
+
+
+def view(layout: Layout, buf=None, dtype="f32", extra=0):
+    esz = L.DTYPES[dtype][1]
+    buf = buf or fake((layout.span() + extra) * esz)
+    return L.TensorView(buf, layout.offset, layout.shape, layout.strides, dtype)
+
+
+def test_library_exports_every_declared_symbol():
+    declared = set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(lg_\w+)\(", HEADER, flags=re.M))
+    assert len(declared) >= 30, declared
+    lib = N.lib()
+    for name in sorted(declared):
+        assert hasattr(lib, name), f"{name} declared in linalg_hip.h but not exported"
+    assert declared == set(N.SIGNATURES), declared ^ set(N.SIGNATURES)
+
+
+def test_no_device_is_reported_not_faked():
+    import torch  # only to learn whether this host has a GPU
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(L.NoDevice):
+        L.Context.new(0)
+
+
+def test_validate_rules():
+    buf = fake(1024 * 4)
+    ok = L.TensorView(buf, 0, [16, 32], [32, 1])
+    ok.validate()
+    with pytest.raises(L.InvalidArgument, match="rank mismatch"):
+        L.TensorView(buf, 0, [16, 32], [32]).validate()
+    cap = buf.nbytes // 4
+    with pytest.raises(L.InvalidArgument, match="buffer holds"):
+        L.TensorView(buf, cap - 100, [16, 32], [32, 1]).validate()
+    with pytest.raises(L.InvalidArgument, match="overflow"):
+        L.TensorView(buf, 0, [4, 5], [2 ** 63, 1]).validate()
+    # Empty views only need the offset inside the buffer.
+    L.TensorView(buf, cap, [0, 5], [5, 1]).validate()
+    with pytest.raises(L.InvalidArgument):
+        L.TensorView(buf, cap + 1, [0, 5], [5, 1]).validate()
+    # Rank 0 is one element at the offset.
+    L.TensorView(buf, cap - 1, [], []).validate()
+    with pytest.raises(L.InvalidArgument):
+        L.TensorView(buf, cap, [], []).validate()
+
+
+def test_may_overlap_is_a_byte_range_test_within_one_allocation():
+    buf = fake(4096 * 4)
+    a = L.TensorView.row_major(buf, 0, [32, 32])
+    b = L.TensorView.row_major(buf, 1024, [32, 32])
+    c = L.TensorView.row_major(buf, 1023, [2])
+    assert not a.may_overlap(b)
+    assert a.may_overlap(c) and c.may_overlap(b)
+    other = L.TensorView.row_major(fake(4096 * 4), 0, [32, 32])
+    assert not a.may_overlap(other)
+    assert not a.may_overlap(L.TensorView.row_major(buf, 0, [0, 3]))
+
+
+def test_permute_view_metadata_matches_the_reference_vector():
+    vp = PKATS["view_path"]
+    v = L.TensorView(fake(1024 * 4), vp["offset"], vp["shape"], vp["strides"])
+    p = P.permute_view(v, vp["perm"])
+    assert p.buffer is v.buffer and p.offset == vp["offset"]
+    assert p.shape == vp["want_shape"] and p.strides == vp["want_strides"]
+    assert p.element_index(vp["index_of"]) == v.element_index(vp["equals_source_index_of"])
+    assert p.len() == v.len()
+
+
+def test_permute_view_round_trip_rank_zero_and_one():
+    v = L.TensorView(fake(4096 * 4), 3, [3, 5, 7, 2], [70, 14, 2, 1])
+    same = P.permute_view(v, [0, 1, 2, 3])
+    assert (same.shape, same.strides) == (v.shape, v.strides)
+    perm = [3, 1, 0, 2]
+    inv = [0] * 4
+    for i, p in enumerate(perm):
+        inv[p] = i
+    back = P.permute_view(P.permute_view(v, perm), inv)
+    assert (back.shape, back.strides, back.offset) == (v.shape, v.strides, v.offset)
+    buf = fake(64)
+    assert P.permute_view(L.TensorView(buf, 2, [], []), []).shape == []
+    assert P.permute_view(L.TensorView.row_major(buf, 0, [9]), [0]).shape == [9]
+
+
+def test_permute_view_rejects_non_permutations():
+    rp = PKATS["rejected_perms"]
+    v = L.TensorView.row_major(fake(1024 * 4), 0, rp["shape"])
+    for bad in rp["perms"]:
+        with pytest.raises(L.InvalidArgument):
+            P.permute_view(v, bad)
+
+
+def test_permutation_plans_for_the_baseline_configs():
+    x = view(Layout.dense([512, 1024, 256]))
+    y = view(Layout.dense([256, 512, 1024]))
+    p = P.plan("materialize", P.permute_view(x, [2, 0, 1]), y)
+    assert p["kind"] == "tile" and p["shape"] == [256, 524288] and p["strides"] == [1, 256]
+    assert (p["axis_a"], p["axis_b"], p["vector"]) == (0, 1, True)
+    x = view(Layout.dense([64, 128, 64, 32]))
+    y = view(Layout.dense([64, 64, 32, 128]))
+    p = P.plan("materialize", P.permute_view(x, [0, 2, 3, 1]), y)
+    assert p["kind"] == "tile" and p["shape"] == [64, 2048, 128]
+    assert p["strides"] == [262144, 1, 2048] and p["axis_a"] == 1 and p["vector"]
+
+
+def test_permutation_path_choice_and_coalescing():
+    # Fully contiguous: one axis, straight copy.
+    x = view(Layout.dense([4, 5, 6]))
+    p = P.plan("materialize", x, view(Layout.dense([4, 5, 6])))
+    assert p["kind"] == "copy" and p["shape"] == [120] and p["vector"]
+    # Last axis unit stride after permuting: copy path (permutation_test.rs:504-505).
+    cm = view(Layout(0, [37, 41], [1, 37]))
+    p = P.plan("materialize", P.permute_view(cm, [1, 0]), view(Layout.dense([41, 37])))
+    assert p["kind"] == "copy"
+    # No unit-stride axis at all: copy path.
+    st = view(Layout(0, [20, 31], [150, 2]))
+    p = P.plan("materialize", P.permute_view(st, [1, 0]), view(Layout.dense([31, 20])))
+    assert p["kind"] == "copy" and p["rank"] == 2
+    # Unit extents vanish; a single element is one axis of extent 1.
+    one = view(Layout.dense([1, 1, 1]))
+    p = P.plan("materialize", P.permute_view(one, [2, 0, 1]), view(Layout.dense([1, 1, 1])))
+    assert p["kind"] == "copy" and p["shape"] == [1]
+    # Misaligned offset: tile path without 128-bit accesses.
+    t = view(Layout(1, [64, 64], [64, 1]), extra=1)
+    p = P.plan("materialize", P.permute_view(t, [1, 0]), view(Layout.dense([64, 64])))
+    assert p["kind"] == "tile" and not p["vector"]
+    # Complex: adjoint conjugates, materialize does not; real adjoint never conjugates.
+    z = view(Layout.dense([3, 5, 37]), dtype="c64")
+    zt = view(Layout.dense([3, 37, 5]), dtype="c64")
+    assert P.plan("adjoint", z, zt)["conj"] and not P.plan("materialize", z, z.__class__(
+        fake(3 * 5 * 37 * 8), 0, [3, 5, 37], [185, 37, 1], "c64"))["conj"]
+    r = view(Layout.dense([3, 5, 37]))
+    assert not P.plan("adjoint", r, view(Layout.dense([3, 37, 5])))["conj"]
+    # Empty shapes plan nothing.
+    e = L.TensorView.row_major(fake(64), 0, [0, 5])
+    ed = L.TensorView.row_major(fake(64), 0, [5, 0])
+    assert P.plan("materialize", P.permute_view(e, [1, 0]), ed)["kind"] == "empty"
+
+
+def test_permutation_error_precedence():
+    src = view(Layout.dense([16, 32]))
+    dbuf = fake(1024 * 4)
+    inv = pytest.raises
+    with inv(L.InvalidArgument, match="does not match"):
+        P.plan("adjoint", src, L.TensorView.row_major(dbuf, 0, [16, 32]))
+    with inv(L.InvalidArgument, match="does not match"):
+        P.plan("materialize", src, L.TensorView.row_major(dbuf, 0, [32, 16]))
+    with inv(L.InvalidArgument, match="contiguous"):
+        P.plan("adjoint", src, L.TensorView(dbuf, 0, [32, 16], [1, 32]))
+    with inv(L.InvalidArgument, match="contiguous"):
+        P.plan("adjoint", src, L.TensorView(dbuf, 0, [32, 16], [20, 1]))
+    cap = dbuf.nbytes // 4
+    with inv(L.InvalidArgument, match="buffer holds"):
+        P.plan("adjoint", src, L.TensorView.row_major(dbuf, cap - 100, [32, 16]))
+    with inv(L.InvalidArgument, match="rank mismatch"):
+        P.plan("adjoint", L.TensorView(src.buffer, 0, [16, 32], [32]),
+               L.TensorView.row_major(dbuf, 0, [32, 16]))
+    with inv(L.InvalidArgument, match="at least 2 axes"):
+        P.plan("adjoint", L.TensorView.row_major(src.buffer, 0, [16]),
+               L.TensorView.row_major(dbuf, 0, [16]))
+    # Overlap: the same buffer in place, or a partially overlapping destination.
+    buf = fake(64 * 64 * 8)
+    a = L.TensorView.row_major(buf, 0, [32, 32], "c64")
+    shifted = L.TensorView.row_major(buf, 100, [32, 32], "c64")
+    for dst in (a, shifted):
+        for op in ("adjoint", "conjugate", "materialize"):
+            with inv(L.Overlap):
+                P.plan(op, a, dst)
+    # A disjoint region of the same buffer is fine.
+    s = L.TensorView.row_major(buf, 0, [37, 41])
+    P.plan("materialize", P.permute_view(s, [1, 0]), L.TensorView.row_major(buf, 2 * 37 * 41, [41, 37]))
+    # More than 8 axes left after coalescing.
+    big = view(Layout.with_([2] * 9, list(range(9)), [2] * 9, 0))
+    with inv(L.InvalidArgument, match="exceeds 8"):
+        P.plan("materialize", big, view(Layout.dense([2] * 9)))
+
+
+def dense(shape, **kw):
+    return view(Layout.dense(shape), **kw)
+
+
+def test_contraction_plans_for_the_baseline_configs():
+    p = C.plan_gemm(1.0, dense([512, 512]), dense([512, 512]), 0.0, dense([512, 512]))
+    assert p["kind"] in ("tiled", "split") and p["a_mode"] == "k" and p["b_mode"] == "mn"
+    # Config 3: B given as a permuted view "bkj" of [32, j, k] storage (unit stride along k).
+    bstore = dense([32, 1024, 1024])
+    bview = P.permute_view(bstore, [0, 2, 1])
+    p = C.plan_contract(1.0, (dense([32, 1024, 1024]), "bik"), (bview, "bkj"), 0.0,
+                        (dense([32, 1024, 1024]), "bij"))
+    assert p["kind"] == "tiled" and p["batch"] == 32 and p["b_mode"] == "k" and p["a_mode"] == "k"
+    # Config 4: tall K goes split-K with a fixed chunk grid.
+    p = C.plan_gemm(1.0, dense([256, 65536]), dense([65536, 256]), 0.0, dense([256, 256]))
+    assert p["kind"] == "split" and p["splits"] > 1 and p["k_chunk"] % 32 == 0
+    assert p["splits"] * p["k_chunk"] >= 65536 > (p["splits"] - 1) * p["k_chunk"]
+    assert p["scratch_bytes"] == p["splits"] * 256 * 256 * 4
+    # Config 5: transpose_matrix views (strides [1, rows]) are read in place.
+    X, W, dY = dense([4096, 4096]), dense([4096, 16384]), dense([4096, 16384])
+    Wt = L.TensorView(W.buffer, 0, [16384, 4096], [1, 16384])
+    Xt = L.TensorView(X.buffer, 0, [4096, 4096], [1, 4096])
+    assert C.plan_gemm(1.0, X, W, 0.0, dense([4096, 16384]))["kind"] == "tiled"
+    p = C.plan_gemm(1.0, dY, Wt, 0.0, dense([4096, 4096]))
+    assert (p["a_mode"], p["b_mode"]) == ("k", "k")
+    p = C.plan_gemm(1.0, Xt, dY, 1.0, dense([4096, 16384]))
+    assert (p["a_mode"], p["b_mode"]) == ("mn", "mn")
+
+
+def test_contraction_plan_kinds_and_edge_semantics():
+    assert C.plan_gemm(1.0, dense([0, 5]), dense([5, 3]), 0.0, dense([0, 3]))["kind"] == "empty"
+    assert C.plan_gemm(1.0, dense([4, 0]), dense([0, 3]), 0.0, dense([4, 3]))["kind"] == "zero"
+    assert C.plan_gemm(1.0, dense([4, 0]), dense([0, 3]), 0.5, dense([4, 3]))["kind"] == "scale"
+    assert C.plan_gemm(0.0, dense([4, 6]), dense([6, 3]), 0.0, dense([4, 3]))["kind"] == "zero"
+    assert C.plan_gemm(0.0, dense([4, 6]), dense([6, 3]), 2.0, dense([4, 3]))["kind"] == "scale"
+    # Collapsible axes merge to one stride per group.
+    p = C.plan_contract(1.0, (dense([2, 3, 2, 3, 2, 3, 5]), "abcdefk"), (dense([5, 7]), "kn"), -0.5,
+                        (dense([2, 3, 2, 3, 2, 3, 7]), "abcdefn"))
+    assert p["kind"] in ("tiled", "split") and p["m"] == 216 and p["groups"] == 1
+    # A scrambled rank-4 contraction keeps several strides: general path.
+    p = C.plan_contract(-1.5, (view(Layout.with_([5, 7, 6, 9], [2, 0, 3, 1], [1] * 4, 3)), "ijkl"),
+                        (view(Layout.with_([9, 6, 4, 11], [3, 0, 2, 1], [1, 2, 1, 1], 0)), "lkmn"),
+                        -0.5, (view(Layout.with_([5, 4, 7, 11], [1, 3, 0, 2], [1, 1, 2, 1], 8)), "imjn"))
+    assert p["kind"] == "general" and p["groups"] > 1
+    # Transposed (column-major) views pick the matching load modes when 16-byte aligned,
+    # and 32-bit predicated loads otherwise.
+    m, n, k = 48, 72, 32
+    p = C.plan_contract(1.0, (view(Layout.transposed(m, k)), "mk"), (view(Layout.transposed(k, n)), "kn"),
+                        0.0, (dense([m, n]), "mn"))
+    assert (p["a_mode"], p["b_mode"]) == ("mn", "k")
+    m, n, k = 45, 70, 33
+    p = C.plan_contract(1.0, (view(Layout.transposed(m, k)), "mk"), (view(Layout.transposed(k, n)), "kn"),
+                        0.0, (dense([m, n]), "mn"))
+    assert (p["a_mode"], p["b_mode"]) == ("strided", "strided")
+    # Odd strides fall back to predicated 32-bit loads.
+    p = C.plan_contract(1.0, (view(Layout.with_([37, 19], [0, 1], [2, 3], 5)), "mk"),
+                        (view(Layout.with_([19, 41], [0, 1], [3, 1], 11)), "kn"), 0.0,
+                        (view(Layout.with_([37, 41], [0, 1], [2, 2], 3)), "mn"))
+    assert (p["a_mode"], p["b_mode"]) == ("strided", "strided")
+    # Split-K sizing depends only on the shape: identical across calls.
+    args = (1.0, dense([4, 300000]), dense([300000, 4]), 0.0, dense([4, 4]))
+    assert C.plan_gemm(*args) == C.plan_gemm(*args)
+
+
+def test_contraction_invalid_metadata():
+    a, b, c = dense([4, 6]), dense([6, 5]), dense([4, 5])
+    inv = lambda: pytest.raises(L.InvalidArgument)
+    ok = lambda la, lb, lc: C.plan_contract(1.0, (a, la), (b, lb), 0.0, (c, lc))
+    ok("mk", "kn", "mn")
+    for la, lb, lc, what in [("mk", "kn", "m", "label count"), ("mkx", "kn", "mn", "label count"),
+                             ("mk", "jn", "mn", "appears once"), ("mk", "kn", "mx", "appears once"),
+                             ("kk", "kn", "mn", "repeated"), ("mk", "kn", "nm", "extent mismatch"),
+                             ("mk", "nk", "mn", "extent mismatch")]:
+        with pytest.raises(L.InvalidArgument, match=what):
+            ok(la, lb, lc)
+    with pytest.raises(L.InvalidArgument, match="only in C"):
+        C.plan_contract(1.0, (a, "mk"), (b, "kn"), 0.0, (dense([4, 5, 2]), "mnx"))
+    with inv():
+        C.plan_gemm(1.0, L.TensorView.row_major(a.buffer, 0, [4, 7]), b, 0.0, c)
+    with pytest.raises(L.InvalidArgument, match="rank below 2"):
+        C.plan_gemm(1.0, L.TensorView.row_major(a.buffer, 0, [6]), b, 0.0, c)
+    with pytest.raises(L.InvalidArgument, match="ranks differ"):
+        C.plan_gemm(1.0, L.TensorView.row_major(a.buffer, 0, [1, 4, 6]), b, 0.0, c)
+    cap = a.buffer.nbytes // 4
+    with inv():
+        C.plan_gemm(1.0, L.TensorView.row_major(a.buffer, cap - 23, [4, 6]), b, 0.0, c)
+    with inv():
+        C.plan_gemm(1.0, a, b, 0.0, L.TensorView(c.buffer, 0, [4, 5], [2 ** 63 - 1, 1]))
+    with inv():
+        C.plan_gemm(1.0, a, b, 0.0, L.TensorView(c.buffer, 0, [4, 5], [5]))
+    # Five M axes whose strides differ between A and C cannot merge below five.
+    wa = dense([2, 2, 2, 2, 2, 3])
+    wb = dense([3, 2])
+    wc = view(Layout.with_([2] * 6, [1, 3, 0, 4, 2, 5], [1] * 6, 0))
+    with pytest.raises(L.InvalidArgument, match="supports 4"):
+        C.plan_contract(1.0, (wa, "abcdek"), (wb, "kn"), 0.0, (wc, "abcden"))
+
+
+def test_contraction_alias_rules():
+    n = 24
+    mbuf = fake(4 * n * n * 4)
+    obuf = fake(n * n * 4)
+    block = lambda r, c_, rows, cols: L.TensorView(mbuf, r * 2 * n + c_, [rows, cols], [2 * n, 1])
+    other = L.TensorView.row_major(obuf, 0, [n, n])
+    whole, shifted, apart = block(0, 0, n, n), block(n - 1, n - 1, n, n), block(n, n, n, n)
+    ov = lambda A, B, Cv: pytest.raises(L.Overlap, match="")
+    for A, B, Cv in [(whole, other, whole), (other, whole, whole), (whole, other, shifted),
+                     (other, shifted, whole)]:
+        with ov(A, B, Cv):
+            C.plan_gemm(1.0, A, B, 0.0, Cv)
+    C.plan_gemm(1.0, whole, whole, 0.0, apart)  # A may alias B
+    column, lower = block(0, 3, n, 1), block(1, 3, n, 1)
+    one = L.TensorView.row_major(obuf, 0, [1, 1])
+    with pytest.raises(L.Overlap):
+        C.plan_gemm(1.0, column, one, 0.0, lower)
+    src = block(0, 0, 4, 4)
+    with pytest.raises(L.Overlap, match="more than once"):
+        C.plan_gemm(1.0, src, src, 0.0, L.TensorView(obuf, 0, [4, 4], [0, 1]))
+    with pytest.raises(L.Overlap, match="more than once"):
+        C.plan_gemm(1.0, src, src, 0.0, L.TensorView(obuf, 0, [4, 4], [1, 1]))
+    # In-place scale is allowed (K = 1 and the other extent 1).
+    col = L.TensorView(mbuf, 8 * 2 * n + 7, [2 * n - 8, 1], [2 * n, 1])
+    piv = L.TensorView.row_major(obuf, 0, [1, 1])
+    assert C.plan_gemm(1.0, col, piv, 0.0, col)["kind"] in ("tiled", "split")
+    row = L.TensorView(mbuf, 3 * 2 * n + 2, [1, 2 * n - 5], [2 * n, 1])
+    assert C.plan_gemm(-0.5, piv, row, 1.0, row)["kind"] in ("tiled", "split")
+    # The LU trailing update: three element-disjoint, byte-interleaved views of one matrix.
+    nn, done, panel = 131, 17, 40
+    lbuf = fake(nn * nn * 4)
+    split = done + panel
+    rest = nn - split
+    Lv = L.TensorView(lbuf, split * nn + done, [rest, panel], [nn, 1])
+    Uv = L.TensorView(lbuf, done * nn + split, [panel, rest], [nn, 1])
+    Cv = L.TensorView(lbuf, split * nn + split, [rest, rest], [nn, 1])
+    assert C.plan_gemm(-1.0, Lv, Uv, 1.0, Cv)["kind"] in ("tiled", "split")
+    # alpha = 0 reads nothing, so aliasing an input is fine there (only C's self-overlap counts).
+    assert C.plan_gemm(0.0, whole, other, 1.0, whole)["kind"] == "scale"

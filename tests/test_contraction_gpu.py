@@ -1,0 +1,516 @@
+"""Contraction parity on the GPU.
+
+Every result is gated componentwise against the f64 reference of
+tests/contraction_test.rs:200-268 with its tolerance
+  |C_gpu - C_ref| <= (K+2)u(|alpha| sum|a||b| + |beta||C0|) + u|C_ref| + tiny,  u = 2^-24,
+and, for 2-D gemm cases, against the crates/cpu restatement with the north-star bound
+  max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|.
+Every buffer element outside C's view must keep its bits; with beta = 0, C starts as NaN.
+The case list restates tests/contraction_test.rs (the 20 typed cases for f32 and the 96-case
+random sweep); the BASELINE configurations run at full size with row samples checked against
+the oracle and size-independent properties (determinism, linearity) on the whole output.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import linalg_hip as L
+import oracle
+from helpers import Case, Layout, Tensor, assert_untouched, rng
+from linalg_hip import contraction as C
+from linalg_hip import permutation as P
+
+pytestmark = pytest.mark.gpu
+
+
+def test_square(ctx, pool):
+    for seed, n in enumerate([1, 8, 64, 96, 100, 256, 384]):
+        Case.matmul(n, n, n).run(ctx, pool, seed)
+    Case.matmul(192, 192, 192).scalars(-1.25, 0.75).run(ctx, pool, 7)
+
+
+def test_unit_extents(ctx, pool):
+    shapes = [(1, 37, 29), (41, 1, 29), (41, 37, 1), (1, 1, 1), (1, 1, 500), (1, 300, 1),
+              (300, 1, 1), (1, 64, 64), (64, 1, 64), (64, 64, 1)]
+    for seed, (m, n, k) in enumerate(shapes):
+        Case.matmul(m, n, k).run(ctx, pool, 100 + seed)
+        Case.matmul(m, n, k).scalars(1.5, -0.5).run(ctx, pool, 200 + seed)
+
+
+def test_zero_k(ctx, pool):
+    for seed, beta in enumerate([0.0, 1.0, -0.5]):
+        Case.matmul(17, 9, 0).scalars(1.0, beta).run(ctx, pool, 300 + seed)
+        batched = Case("batched K=0", (Layout.dense([3, 5, 0, 2]), "bmkl"),
+                       (Layout.dense([3, 0, 2, 4]), "bkln"), (Layout.dense([3, 5, 4]), "bmn"))
+        batched.scalars(2.0, beta).run(ctx, pool, 310 + seed)
+
+
+def test_empty_output(ctx, pool):
+    for seed, (m, n, k) in enumerate([(0, 5, 3), (5, 0, 3), (0, 0, 0), (0, 4, 0)]):
+        Case.matmul(m, n, k).scalars(1.0, -0.5).run(ctx, pool, 400 + seed)
+    Case("empty batch", (Layout.dense([0, 4, 3]), "bmk"), (Layout.dense([0, 3, 5]), "bkn"),
+         (Layout.dense([0, 4, 5]), "bmn")).run(ctx, pool, 410)
+
+
+def test_prime_sizes(ctx, pool):
+    Case.matmul(127, 251, 63).run(ctx, pool, 500)
+    Case.matmul(127, 251, 63).scalars(-0.75, 1.0).run(ctx, pool, 501)
+    Case.matmul(251, 127, 67).scalars(0.5, -0.5).run(ctx, pool, 502)
+    Case.matmul(257, 131, 129).scalars(1.0, 0.0).run(ctx, pool, 503)
+
+
+def test_transposed_views(ctx, pool):
+    for (m, n, k) in [(45, 70, 33), (48, 72, 32), (130, 260, 96)]:
+        pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+        for mask in range(8):
+            ta, tb, tc = bool(mask & 1), bool(mask & 2), bool(mask & 4)
+            case = Case(f"transposed a={ta} b={tb} c={tc} {m}x{n}x{k}", (pick(ta, m, k), "mk"),
+                        (pick(tb, k, n), "kn"), (pick(tc, m, n), "mn"))
+            case.scalars(1.0, 0.0 if mask % 2 == 0 else -0.5).run(ctx, pool, 600 + mask)
+    via = Case.matmul(45, 70, 33)
+    via.a = (Layout.transposed(45, 33), "mk")
+    via.c = (Layout.transposed(45, 70), "mn")
+    via.run(ctx, pool, 610)
+
+
+def test_strided_views(ctx, pool):
+    m, n, k = 37, 41, 19
+    layouts = [
+        (Layout.with_([m, k], [0, 1], [2, 3], 5), Layout.with_([k, n], [0, 1], [3, 1], 11),
+         Layout.with_([m, n], [0, 1], [2, 2], 3)),
+        (Layout.with_([m, k], [1, 0], [1, 2], 1), Layout.with_([k, n], [1, 0], [2, 2], 9),
+         Layout.with_([m, n], [1, 0], [3, 1], 17)),
+        (Layout.with_([m, k], [0, 1], [1, 1], 64), Layout.with_([k, n], [0, 1], [1, 1], 1),
+         Layout.with_([m, n], [0, 1], [1, 1], 77)),
+    ]
+    for seed, (a, b, c) in enumerate(layouts):
+        for alpha, beta in [(1.0, 0.0), (-2.0, 1.0), (0.5, -0.5)]:
+            Case(f"strided #{seed}", (a, "mk"), (b, "kn"), (c, "mn")).scalars(alpha, beta).run(
+                ctx, pool, 700 + seed)
+    via = Case.matmul(70, 70, 70)
+    via.a = (Layout.with_([70, 70], [0, 1], [1, 2], 3), "mk")
+    via.b = (Layout.with_([70, 70], [1, 0], [2, 1], 6), "kn")
+    via.c = (Layout.with_([70, 70], [0, 1], [3, 1], 9), "mn")
+    via.scalars(1.0, -0.5).run(ctx, pool, 710)
+
+
+def test_batched(ctx, pool):
+    for seed, batch in enumerate([[3], [2, 3], [1, 1, 5], [70]]):
+        m, n, k = 33, 20, 17
+        labels = "xyz"[: len(batch)]
+        case = Case(f"batched gemm {batch}", (Layout.dense(batch + [m, k]), labels + "mk"),
+                    (Layout.dense(batch + [k, n]), labels + "kn"),
+                    (Layout.dense(batch + [m, n]), labels + "mn"), via_gemm=True)
+        case.scalars(1.0, 0.0 if seed % 2 == 0 else -0.5).run(ctx, pool, 800 + seed)
+    Case("batch axis in the middle", (Layout.with_([19, 6, 23], [1, 0, 2], [1, 1, 1], 2), "mbk"),
+         (Layout.with_([23, 31, 6], [0, 2, 1], [1, 1, 2], 0), "knb"),
+         (Layout.with_([31, 6, 19], [1, 2, 0], [1, 1, 1], 4), "nbm")).scalars(0.5, -0.5).run(ctx, pool, 810)
+    Case("many small matrices", (Layout.dense([500, 4, 3]), "bmk"), (Layout.dense([500, 3, 5]), "bkn"),
+         (Layout.dense([500, 4, 5]), "bmn")).run(ctx, pool, 811)
+    Case("one B for every A", (Layout.dense([7, 21, 40]), "bmk"), (Layout.dense([40, 13]), "kn"),
+         (Layout.dense([7, 21, 13]), "bmn")).scalars(1.0, 1.0).run(ctx, pool, 812)
+
+
+def test_rank4_two_axes(ctx, pool):
+    i, j, k, l, m, n = 5, 7, 6, 9, 4, 11
+    Case("ijkl,klmn->ijmn dense", (Layout.dense([i, j, k, l]), "ijkl"),
+         (Layout.dense([k, l, m, n]), "klmn"), (Layout.dense([i, j, m, n]), "ijmn")).run(ctx, pool, 900)
+    Case("ijkl,lkmn->imjn scrambled",
+         (Layout.with_([i, j, k, l], [2, 0, 3, 1], [1, 1, 1, 1], 3), "ijkl"),
+         (Layout.with_([l, k, m, n], [3, 0, 2, 1], [1, 2, 1, 1], 0), "lkmn"),
+         (Layout.with_([i, m, j, n], [1, 3, 0, 2], [1, 1, 2, 1], 8), "imjn")).scalars(-1.5, -0.5).run(ctx, pool, 901)
+    i, j, k, l, m, n = 9, 10, 12, 11, 8, 13
+    Case("ijkl,mlkn->njim larger", (Layout.dense([i, j, k, l]), "ijkl"),
+         (Layout.dense([m, l, k, n]), "mlkn"), (Layout.dense([n, j, i, m]), "njim")).scalars(1.0, 1.0).run(ctx, pool, 902)
+
+
+def test_collapsible_axes(ctx, pool):
+    Case("six collapsible M axes", (Layout.dense([2, 3, 2, 3, 2, 3, 5]), "abcdefk"),
+         (Layout.dense([5, 7]), "kn"), (Layout.dense([2, 3, 2, 3, 2, 3, 7]), "abcdefn")).scalars(1.0, -0.5).run(ctx, pool, 1000)
+    Case("unit axes everywhere",
+         (Layout.with_([1, 6, 1, 1, 9, 1], [5, 3, 1, 0, 2, 4], [1, 2, 1, 3, 1, 1], 1), "pmqrks"),
+         (Layout.with_([1, 9, 1, 1, 8, 1], [0, 4, 2, 1, 3, 5], [2, 1, 1, 1, 1, 4], 0), "skrtnq"),
+         (Layout.with_([1, 1, 6, 8, 1, 1], [3, 2, 0, 1, 4, 5], [1, 1, 1, 1, 1, 1], 2), "tpmnsq")).run(ctx, pool, 1001)
+
+
+def test_beta_variants(ctx, pool):
+    seed = 1100
+    for m, n, k in [(70, 50, 40), (33, 65, 1), (5, 6, 20000)]:
+        for beta in [0.0, 1.0, -0.5]:
+            for alpha in [1.0, -2.5]:
+                Case.matmul(m, n, k).scalars(alpha, beta).run(ctx, pool, seed)
+                seed += 1
+
+
+def test_split_k(ctx, pool):
+    shapes = [(1, 1, 1000003), (8, 8, 65536), (3, 5, 200001), (40, 24, 30000), (1, 70, 9973),
+              (130, 200, 20000)]
+    for seed, (m, n, k) in enumerate(shapes):
+        Case.matmul(m, n, k).run(ctx, pool, 1200 + seed)
+        Case.matmul(m, n, k).scalars(0.5, -0.5).run(ctx, pool, 1210 + seed)
+    Case("batched long K", (Layout.with_([3, 2, 50000], [2, 0, 1], [1, 1, 1], 1), "bmk"),
+         (Layout.dense([3, 50000, 4]), "bkn"), (Layout.dense([3, 2, 4]), "bmn")).scalars(-1.0, 1.0).run(ctx, pool, 1220)
+
+
+def test_deterministic(ctx, pool):
+    for seed, (m, n, k) in enumerate([(4, 4, 300000), (130, 70, 90), (9, 1, 1), (256, 256, 65536)]):
+        g = rng(1300 + seed)
+        a = Tensor.random(pool, Layout.dense([m, k]), g)
+        b = Tensor.random(pool, Layout.dense([k, n]), g)
+        runs = []
+        for _ in range(3):
+            c = Tensor(pool, Layout.dense([m, n]))
+            C.gemm(ctx, 1.0, a.view(), b.view(), 0.0, c.view())
+            runs.append(c.read().view(np.uint32).copy())
+        assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[1], runs[2]), (m, n, k)
+
+
+def test_non_finite_inputs(ctx, pool):
+    for seed, (m, n, k) in enumerate([(70, 45, 50), (3, 2, 40000), (9, 11, 1), (200, 150, 300)]):
+        g = rng(1400 + seed)
+        a = Tensor.random(pool, Layout.dense([m, k]), g)
+        b = Tensor.random(pool, Layout.dense([k, n]), g)
+        c = Tensor(pool, Layout.dense([m, n]))
+        nan_row, inf_col = m - 1, n - 2
+        a.host[nan_row * k + (k - 1)] = np.nan
+        b.host[(k // 2) * n + inf_col] = np.inf
+        a.upload()
+        b.upload()
+        c0 = c.host.copy()
+        e = oracle.contract_f64(1.0, a.host, a.layout.tup(), "mk", b.host, b.layout.tup(), "kn",
+                                0.0, c0, c.layout.tup(), "mn")
+        C.gemm(ctx, 1.0, a.view(), b.view(), 0.0, c.view())
+        got = c.read()
+        name = f"non-finite {m}x{n}x{k}"
+        oracle.gate(got, e, name)
+        out = got[: m * n].reshape(m, n)
+        poisoned = np.zeros((m, n), bool)
+        poisoned[nan_row, :] = True
+        poisoned[:, inf_col] = True
+        assert np.array_equal(np.isfinite(out), ~poisoned), name
+
+
+def test_alpha_zero(ctx, pool):
+    for seed, (m, n, k) in enumerate([(20, 30, 40), (2, 2, 50000), (7, 5, 1)]):
+        for beta in [0.0, 1.0, -0.5]:
+            g = rng(1500 + seed)
+            a = Tensor(pool, Layout.dense([m, k]), np.full(m * k + 13, np.nan, np.float32))
+            b = Tensor(pool, Layout.dense([k, n]), np.full(k * n + 13, np.nan, np.float32))
+            c = Tensor.random(pool, Layout.dense([m, n]), g)
+            c0 = c.host.copy()
+            C.gemm(ctx, 0.0, a.view(), b.view(), beta, c.view())
+            got = c.read()[: m * n]
+            want = (np.float32(beta) * c0[: m * n]).astype(np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, n, k, beta)
+
+
+def test_lu_trailing_update(ctx, pool):
+    for seed, (n, done, panel) in enumerate([(96, 0, 32), (131, 17, 40), (64, 5, 1)]):
+        g = rng(1600 + seed)
+        mat = Tensor.random(pool, Layout.dense([n, n]), g)
+        split = done + panel
+        rest = n - split
+        l_ = Layout(split * n + done, [rest, panel], [n, 1])
+        u_ = Layout(done * n + split, [panel, rest], [n, 1])
+        c_ = Layout(split * n + split, [rest, rest], [n, 1])
+        before = mat.host.copy()
+        e = oracle.contract_f64(-1.0, before, l_.tup(), "mk", before, u_.tup(), "kn", 1.0, before,
+                                c_.tup(), "mn")
+        mk = lambda lay: L.TensorView(mat.buffer, lay.offset, lay.shape, lay.strides)
+        C.gemm(ctx, -1.0, mk(l_), mk(u_), 1.0, mk(c_))
+        got = mat.read()
+        name = f"LU trailing update n={n} panel={panel}"
+        assert_untouched(name, before, got, e.index)
+        oracle.gate(got, e, name)
+
+
+def test_in_place_scale(ctx, pool):
+    n, col, top = 50, 7, 8
+    g = rng(1700)
+    mat = Tensor.random(pool, Layout.dense([n, n]), g)
+    piv = Tensor.random(pool, Layout.dense([1, 1]), g)
+    column = Layout(top * n + col, [n - top, 1], [n, 1])
+    before = mat.host.copy()
+    e = oracle.contract_f64(1.0, before, column.tup(), "mk", piv.host, piv.layout.tup(), "kn", 0.0,
+                            before, column.tup(), "mn")
+    v = L.TensorView(mat.buffer, column.offset, column.shape, column.strides)
+    C.gemm(ctx, 1.0, v, piv.view(), 0.0, v)
+    got = mat.read()
+    assert_untouched("in-place column scale", before, got, e.index)
+    oracle.gate(got, e, "in-place column scale")
+    row = Layout(3 * n + 2, [1, n - 5], [n, 1])
+    before = got.copy()
+    mat.host[:] = before
+    e = oracle.contract_f64(-0.5, piv.host, piv.layout.tup(), "mk", before, row.tup(), "kn", 1.0,
+                            before, row.tup(), "mn")
+    v = L.TensorView(mat.buffer, row.offset, row.shape, row.strides)
+    C.gemm(ctx, -0.5, piv.view(), v, 1.0, v)
+    got = mat.read()
+    assert_untouched("in-place row scale", before, got, e.index)
+    oracle.gate(got, e, "in-place row scale")
+
+
+def test_overlap_rejected_without_launch(ctx, pool):
+    n = 24
+    g = rng(1800)
+    mat = Tensor.random(pool, Layout.dense([2 * n, 2 * n]), g)
+    other = Tensor.random(pool, Layout.dense([n, n]), g)
+    block = lambda r, c_, rows, cols: L.TensorView(mat.buffer, r * 2 * n + c_, [rows, cols], [2 * n, 1])
+    whole, shifted, apart = block(0, 0, n, n), block(n - 1, n - 1, n, n), block(n, n, n, n)
+    n0 = ctx.launches()
+    for A, B, Cv in [(whole, other.view(), whole), (other.view(), whole, whole),
+                     (whole, other.view(), shifted), (other.view(), shifted, whole)]:
+        with pytest.raises(L.Overlap):
+            C.gemm(ctx, 1.0, A, B, 0.0, Cv)
+    src = block(0, 0, 4, 4)
+    for bad in ([0, 1], [1, 1]):
+        with pytest.raises(L.Overlap):
+            C.gemm(ctx, 1.0, src, src, 0.0, L.TensorView(other.buffer, 0, [4, 4], bad))
+    assert ctx.launches() == n0
+    assert np.array_equal(mat.read().view(np.uint32), mat.host.view(np.uint32))
+    assert np.array_equal(other.read().view(np.uint32), other.host.view(np.uint32))
+    C.gemm(ctx, 1.0, whole, whole, 0.0, apart)  # A may alias B
+    got = mat.read()
+    e = oracle.contract_f64(1.0, mat.host, (0, [n, n], [2 * n, 1]), "mk", mat.host,
+                            (0, [n, n], [2 * n, 1]), "kn", 0.0, mat.host,
+                            (n * 2 * n + n, [n, n], [2 * n, 1]), "mn")
+    oracle.gate(got, e, "A aliases B")
+
+
+def test_invalid_metadata_without_launch(ctx, pool):
+    g = rng(1900)
+    a = Tensor.random(pool, Layout.dense([4, 6]), g)
+    b = Tensor.random(pool, Layout.dense([6, 5]), g)
+    c = Tensor.random(pool, Layout.dense([4, 5]), g)
+    av, bv, cv = a.view(), b.view(), c.view()
+    C.contract(ctx, 1.0, (av, "mk"), (bv, "kn"), 0.0, (cv, "mn"))
+    c1 = c.read()
+    assert not np.array_equal(c1, c.host)
+    n0 = ctx.launches()
+    for la, lb, lc in [("mk", "kn", "m"), ("mkx", "kn", "mn"), ("mk", "jn", "mn"),
+                       ("kk", "kn", "mn"), ("mk", "kn", "nm"), ("mk", "nk", "mn")]:
+        with pytest.raises(L.InvalidArgument):
+            C.contract(ctx, 1.0, (av, la), (bv, lb), 0.0, (cv, lc))
+    with pytest.raises(L.InvalidArgument):
+        C.gemm(ctx, 1.0, L.TensorView.row_major(a.buffer, 0, [4, 7]), bv, 0.0, cv)
+    with pytest.raises(L.InvalidArgument):
+        C.encode_gemm(ctx, ctx.queue, 1.0, L.TensorView.row_major(a.buffer, 0, [4, 7]), bv, 0.0, cv)
+    with pytest.raises(L.InvalidArgument):
+        C.encode_contract(ctx, ctx.queue, 1.0, (av, "mk"), (bv, "kn"), 0.0, (cv, "m"))
+    ctx.sync()
+    assert ctx.launches() == n0
+    assert np.array_equal(c.read().view(np.uint32), c1.view(np.uint32))
+
+
+def test_shared_stream_orders_dependent_work(ctx, pool):
+    m, k, n, p = 37, 29, 43, 3
+    g = rng(2000)
+    a = Tensor.random(pool, Layout.dense([m, k]), g)
+    b = Tensor.random(pool, Layout.dense([k, n]), g)
+    d = Tensor.random(pool, Layout.transposed(n, p), g)
+    long = Tensor.random(pool, Layout.dense([2, 40000]), g)
+    ab = Tensor.random(pool, Layout.dense([m, n]), g)
+    abd = Tensor.random(pool, Layout.dense([m, p]), g)
+    gram = Tensor.random(pool, Layout.dense([2, 2]), g)
+    ab0, abd0, gram0 = ab.host.copy(), abd.host.copy(), gram.host.copy()
+    s = ctx.new_stream()
+    try:
+        C.encode_gemm(ctx, s, 1.0, a.view(), b.view(), 0.0, ab.view())
+        C.encode_contract(ctx, s, 0.5, (ab.view(), "mn"), (d.view(), "np"), -0.5, (abd.view(), "mp"))
+        C.encode_contract(ctx, s, 1.0, (long.view(), "ik"), (long.view(), "jk"), 1.0, (gram.view(), "ij"))
+        s.wait_until_completed()
+    finally:
+        s.close()
+    ab1 = ab.read()
+    oracle.gate(ab1, oracle.contract_f64(1.0, a.host, a.layout.tup(), "mk", b.host, b.layout.tup(), "kn",
+                                         0.0, ab0, ab.layout.tup(), "mn"), "A.B")
+    oracle.gate(abd.read(), oracle.contract_f64(0.5, ab1, ab.layout.tup(), "mn", d.host, d.layout.tup(),
+                                                "np", -0.5, abd0, abd.layout.tup(), "mp"), "(A.B).D")
+    oracle.gate(gram.read(), oracle.contract_f64(1.0, long.host, long.layout.tup(), "ik", long.host,
+                                                 long.layout.tup(), "jk", 1.0, gram0, gram.layout.tup(),
+                                                 "ij"), "Gram")
+
+
+# --------------------------------------------------------------------------------------
+# Random einsum sweep (tests/contraction_test.rs:1008-1096), own seeded generator.
+# --------------------------------------------------------------------------------------
+def random_operand(labels, g):
+    logical = list(labels)
+    order = list(range(len(logical)))
+    for i in range(len(logical) - 1, 0, -1):
+        j = int(g.integers(0, i + 1))
+        logical[i], logical[j] = logical[j], logical[i]
+        j = int(g.integers(0, i + 1))
+        order[i], order[j] = order[j], order[i]
+    shape = [n for _, n in logical]
+    steps = [int(g.integers(1, 3)) for _ in shape]
+    return Layout.with_(shape, order, steps, int(g.integers(0, 8))), "".join(l for l, _ in logical)
+
+
+def test_random_contractions(ctx, pool):
+    g = rng(0xC0FFEE)
+    for case_no in range(96):
+        def extent():
+            r = g.integers(0, 12)
+            if r == 0:
+                return 0
+            if r <= 2:
+                return 1
+            if r <= 10:
+                return int(g.integers(2, 7))
+            return int(g.integers(17, 41))
+        groups = [[extent() for _ in range(int(g.integers(0, 3)))] for _ in range(4)]
+        while np.prod([max(n, 1) for grp in groups for n in grp]) > 400000:
+            flat = [(n, gi, i) for gi, grp in enumerate(groups) for i, n in enumerate(grp)]
+            n, gi, i = max(flat)
+            groups[gi][i] = (n + 1) // 2
+        names = iter("abcdefgh")
+        lab = [[(next(names), n) for n in grp] for grp in groups]
+        batch, m, n, k = lab
+        lg = rng(int(g.integers(0, 2 ** 63)))
+        a, la = random_operand(batch + m + k, lg)
+        b, lb = random_operand(batch + n + k, lg)
+        c, lc = random_operand(batch + m + n, lg)
+        alpha = [1.0, -0.75, 0.0][int(g.integers(0, 3))]
+        beta = [0.0, 1.0, -0.5][int(g.integers(0, 3))]
+        Case(f"random #{case_no} {la},{lb}->{lc} {groups}", (a, la), (b, lb), (c, lc)).scalars(
+            alpha, beta).run(ctx, pool, int(lg.integers(0, 2 ** 31)))
+
+
+def test_tile_edge_sweep(ctx, pool):
+    """Ragged M/N/K around the 128x128x32 tile and the 64-row wave tile."""
+    seed = 5000
+    for m in [1, 31, 32, 33, 63, 64, 65, 127, 128, 129]:
+        for n in [1, 33, 64, 127, 129]:
+            for k in [1, 7, 31, 32, 33, 64, 100]:
+                if (m * n * k) % 3:
+                    continue
+                alpha, beta = [(1.0, 0.0), (-0.75, 1.0), (0.5, -0.5), (2.0, 0.0)][seed % 4]
+                Case.matmul(m, n, k).scalars(alpha, beta).run(ctx, pool, seed)
+                seed += 1
+
+
+# --------------------------------------------------------------------------------------
+# BASELINE configurations at full size
+# --------------------------------------------------------------------------------------
+def _rows_check(name, got_rows, want_rows, k, amax, bmax):
+    tol = 1e-5 * np.sqrt(k) * amax * bmax
+    err = float(np.max(np.abs(got_rows.astype(np.float64) - want_rows.astype(np.float64))))
+    assert err <= tol, f"{name}: max|err| {err:e} > {tol:e}"
+    return err
+
+
+def test_config1_gemm_512_full_oracle(ctx, pool):
+    m = n = k = 512
+    g = rng(1)
+    a = g.uniform(-1, 1, m * k).astype(np.float32)
+    b = rng(2).uniform(-1, 1, k * n).astype(np.float32)
+    A, B, Cc = (Tensor(pool, Layout.dense(s), d) for s, d in
+                (([m, k], a), ([k, n], b), ([m, n], np.zeros(m * n, np.float32))))
+    C.gemm(ctx, 1.0, A.view(), B.view(), 0.0, Cc.view())
+    got = Cc.read()[: m * n]
+    ref = np.zeros(m * n, np.float32)
+    oracle.gemm_fast(m, n, k, 1.0, 0.0, a, 0, (k, 1), b, 0, (n, 1), ref, 0, (n, 1))
+    _rows_check("config 1", got, ref, k, 1.0, 1.0)
+    e = oracle.contract_f64(1.0, a, (0, [m, k], [k, 1]), "mk", b, (0, [k, n], [n, 1]), "kn", 0.0,
+                            ref, (0, [m, n], [n, 1]), "mn")
+    oracle.gate(got, e, "config 1")
+
+
+def test_config3_batched_with_permuted_b(ctx, pool):
+    bsz, m = 32, 1024
+    g = rng(5)
+    a = g.uniform(-1, 1, bsz * m * m).astype(np.float32)
+    bstore = rng(6).uniform(-1, 1, bsz * m * m).astype(np.float32)  # [b, j, k]
+    A = Tensor(pool, Layout.dense([bsz, m, m]), a)
+    Bs = Tensor(pool, Layout.dense([bsz, m, m]), bstore)
+    Cc = Tensor(pool, Layout.dense([bsz, m, m]))
+    bview = P.permute_view(Bs.view(), [0, 2, 1])  # "bkj": strides [2^20, 1, 1024]
+    assert bview.strides == [m * m, 1, m]
+    plan = C.plan_contract(1.0, (A.view(), "bik"), (bview, "bkj"), 0.0, (Cc.view(), "bij"))
+    assert plan["kind"] == "tiled" and plan["b_mode"] == "k"
+    C.contract(ctx, 1.0, (A.view(), "bik"), (bview, "bkj"), 0.0, (Cc.view(), "bij"))
+    got = Cc.read()[: bsz * m * m]
+    rows = rng(55).choice(m, 16, replace=False)
+    for bi in [0, 13, 31]:
+        ref = np.zeros(m * m, np.float32)
+        # crates/cpu layout (RM, Transposed, RM): B[k][j] = Bstore[j][k], strides [1, K].
+        oracle.gemm_fast(m, m, m, 1.0, 0.0, a, bi * m * m, (m, 1), bstore, bi * m * m, (1, m),
+                         ref, 0, (m, 1), rows=rows)
+        for r in rows:
+            _rows_check(f"config 3 batch {bi} row {r}", got[bi * m * m + r * m: bi * m * m + (r + 1) * m],
+                        ref[r * m:(r + 1) * m], m, 1.0, 1.0)
+
+
+def test_config4_split_k_full_oracle_and_deterministic(ctx, pool):
+    m = n = 256
+    k = 65536
+    sigma = 1.0 / np.sqrt(k)
+    a = (rng(7).standard_normal(m * k) * sigma).astype(np.float32)
+    b = (rng(8).standard_normal(k * n) * sigma).astype(np.float32)
+    A = Tensor(pool, Layout.dense([m, k]), a)
+    B = Tensor(pool, Layout.dense([k, n]), b)
+    plan = C.plan_gemm(1.0, A.view(), B.view(), 0.0, Tensor(pool, Layout.dense([m, n])).view())
+    assert plan["kind"] == "split"
+    outs = []
+    for _ in range(3):
+        Cc = Tensor(pool, Layout.dense([m, n]))
+        C.gemm(ctx, 1.0, A.view(), B.view(), 0.0, Cc.view())
+        outs.append(Cc.read()[: m * n].copy())
+    assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])
+    ref = np.zeros(m * n, np.float32)
+    oracle.gemm_fast(m, n, k, 1.0, 0.0, a, 0, (k, 1), b, 0, (n, 1), ref, 0, (n, 1))
+    _rows_check("config 4", outs[0], ref, k, float(np.abs(a).max()), float(np.abs(b).max()))
+
+
+def test_config5_linear_layer_step(ctx, pool):
+    """One 1F1B stage's linear step: Y = X.W, dX = dY.W^T, dW += X^T.dY (transposed views)."""
+    M, K, N = 4096, 4096, 16384
+    x = (rng(9).standard_normal(M * K) * 0.02).astype(np.float32)
+    w = (rng(10).standard_normal(K * N) * 0.02).astype(np.float32)
+    dy = (rng(11).standard_normal(M * N) * 0.02).astype(np.float32)
+    X = Tensor(pool, Layout.dense([M, K]), x)
+    W = Tensor(pool, Layout.dense([K, N]), w)
+    DY = Tensor(pool, Layout.dense([M, N]), dy)
+    Y = Tensor(pool, Layout.dense([M, N]))
+    DX = Tensor(pool, Layout.dense([M, K]))
+    DW = Tensor(pool, Layout.dense([K, N]))
+    Wt = L.TensorView(W.buffer, 0, [N, K], [1, N])   # transpose_matrix(W)
+    Xt = L.TensorView(X.buffer, 0, [K, M], [1, K])   # transpose_matrix(X)
+    C.gemm(ctx, 1.0, X.view(), W.view(), 0.0, Y.view())
+    C.gemm(ctx, 1.0, DY.view(), Wt, 0.0, DX.view())
+    C.gemm(ctx, 1.0, Xt, DY.view(), 1.0, DW.view())   # dW starts at zero, beta = 1 accumulates
+    y, dx, dw = Y.read(), DX.read(), DW.read()
+    rows = rng(99).choice(M, 8, replace=False)
+    ax, aw, ady = (float(np.abs(t).max()) for t in (x, w, dy))
+    ref = np.zeros(M * N, np.float32)
+    oracle.gemm_fast(M, N, K, 1.0, 0.0, x, 0, (K, 1), w, 0, (N, 1), ref, 0, (N, 1), rows=rows)
+    for r in rows:
+        _rows_check(f"Y row {r}", y[r * N:(r + 1) * N], ref[r * N:(r + 1) * N], K, ax, aw)
+    ref = np.zeros(M * K, np.float32)
+    oracle.gemm_fast(M, K, N, 1.0, 0.0, dy, 0, (N, 1), w, 0, (1, N), ref, 0, (K, 1), rows=rows)
+    for r in rows:
+        _rows_check(f"dX row {r}", dx[r * K:(r + 1) * K], ref[r * K:(r + 1) * K], N, ady, aw)
+    ref = np.zeros(K * N, np.float32)
+    oracle.gemm_fast(K, N, M, 1.0, 1.0, x, 0, (1, K), dy, 0, (N, 1), ref, 0, (N, 1), rows=rows)
+    for r in rows:
+        _rows_check(f"dW row {r}", dw[r * N:(r + 1) * N], ref[r * N:(r + 1) * N], M, ax, ady)
+
+
+def test_gemm_4096_cubed_rows_and_linearity(ctx, pool):
+    n = 4096
+    a = rng(12).uniform(-1, 1, n * n).astype(np.float32)
+    b = rng(13).uniform(-1, 1, n * n).astype(np.float32)
+    A, B = Tensor(pool, Layout.dense([n, n]), a), Tensor(pool, Layout.dense([n, n]), b)
+    C1, C2 = Tensor(pool, Layout.dense([n, n])), Tensor(pool, Layout.dense([n, n]))
+    C.gemm(ctx, 1.0, A.view(), B.view(), 0.0, C1.view())
+    # Linearity: C2 = 2*A.B computed as alpha = 2 must be exactly twice C1 (power-of-two scale).
+    C.gemm(ctx, 2.0, A.view(), B.view(), 0.0, C2.view())
+    c1, c2 = C1.read()[: n * n], C2.read()[: n * n]
+    assert np.array_equal((c1 * np.float32(2)).view(np.uint32), c2.view(np.uint32))
+    rows = rng(77).choice(n, 8, replace=False)
+    ref = np.zeros(n * n, np.float32)
+    oracle.gemm_fast(n, n, n, 1.0, 0.0, a, 0, (n, 1), b, 0, (n, 1), ref, 0, (n, 1), rows=rows)
+    for r in rows:
+        _rows_check(f"4096^3 row {r}", c1[r * n:(r + 1) * n], ref[r * n:(r + 1) * n], n, 1.0, 1.0)
