@@ -93,7 +93,7 @@ class Tensor:
         self.buffer = pool.alloc("f32", self.cap)
         self.host = np.zeros(self.buffer.nbytes // 4, dtype=np.float32)
         if data is not None:
-            self.host[: self.cap] = data
+            self.host[: data.size] = data
         self.buffer.write(self.host)
 
     @classmethod
