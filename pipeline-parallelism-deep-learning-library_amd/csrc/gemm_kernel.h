@@ -1,0 +1,280 @@
+// The fp32 MFMA GEMM kernel of the contraction path, parameterized by pipeline shape.
+//
+// gemm_f32_mfma<AM, BMD, BK, PIPE>: C = alpha * A.B + beta * C (or raw split-K partials) for
+// one stride per group. 128x128 output tile per 256-thread workgroup (4 waves in 2x2, each
+// wave 64x64 = 2x2 blocks of v_mfma_f32_32x32x2_f32 accumulating in fp32). K advances BK at a
+// time through two LDS stages: while the MFMAs consume stage s, the next K-slice is already in
+// flight from HBM into registers, and is written to stage s^1 before the one barrier per
+// slice. Operand loads follow the operand's unit-stride axis so a transposed or permuted
+// view is read as it lies, 128 bits per load:
+//   LOAD_K  : unit stride along K   -> LDS [row][k] (pitch BK+4), 128-bit LDS reads along k
+//   LOAD_MN : unit stride along M/N -> LDS [k][row] (pitch 136), 32-bit LDS reads
+//   LOAD_S  : anything else         -> 32-bit predicated loads into the [row][k] layout
+// Inside a K-slice, MFMA step s of lane half h uses k = 8*(s/4) + 4*h + s%4, so a [row][k]
+// stage hands each lane four consecutive k with one ds_read_b128. A and B agree on this order,
+// so every product pairs the same k. With PIPE, the LDS fragments of step group g+1 are read
+// while the 16 MFMAs of group g run (register double buffer), hiding LDS latency.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "lg_internal.h"
+
+namespace lg {
+namespace gemm_detail {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = GEMM_BM, BN = GEMM_BN;
+constexpr int PMN = BM + 8;  // pitch of a [k][row] stage (floats)
+static_assert(BM == 128 && BN == 128, "the wave layout below assumes 128x128 tiles");
+
+template <int BK>
+struct Geo {
+    static constexpr int PK = BK + 4;                           // pitch of a [row][k] stage
+    static constexpr int LOADS = (BM * BK / 4) / GEMM_THREADS;  // 128-bit loads per thread
+    static_assert(LOADS * GEMM_THREADS * 4 == BM * BK, "tile must split evenly over threads");
+    template <int MODE>
+    static constexpr int stage() { return MODE == LOAD_MN ? BK * PMN : BM * PK; }
+};
+
+// Workgroup -> (plane, tile_m, tile_n). Workgroups are dealt round-robin to the 8 XCDs, so
+// the linear id is first regrouped so each XCD owns one contiguous run of tiles (sharing
+// its L2), then tiles within a plane are walked in groups of 8 tile-rows for A/B reuse.
+__device__ inline void decode_tile(uint32_t bid, uint32_t total, uint32_t tiles_m,
+                                   uint32_t tiles_n, uint32_t* plane, uint32_t* tm,
+                                   uint32_t* tn) {
+    const uint32_t xcd = bid & 7u, slot = bid >> 3;
+    const uint32_t q = total >> 3, r = total & 7u;
+    const uint32_t lin = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+    const uint32_t per_plane = tiles_m * tiles_n;
+    *plane = lin / per_plane;
+    const uint32_t t = lin - *plane * per_plane;
+    constexpr uint32_t GROUP = 8;
+    const uint32_t group_size = GROUP * tiles_n;
+    const uint32_t group = t / group_size;
+    const uint32_t first_m = group * GROUP;
+    const uint32_t gm = min(tiles_m - first_m, GROUP);
+    const uint32_t in_group = t - group * group_size;
+    *tm = first_m + in_group % gm;
+    *tn = in_group / gm;
+}
+
+// Loads one operand's K-slice (rows [0, rows_left) x k [k0, k0+BK) within klen) into
+// registers. `p` points at (row 0, k 0) of the tile; srow/sk are the operand's strides.
+// FULL (workgroup-uniform: the whole slice is inside the operand) takes branch-free 128-bit
+// loads so every load of the slice is in flight at once; edge slices predicate each element.
+template <int MODE, bool FULL, int BK>
+__device__ inline void load_slice(floatx4 (&r)[Geo<BK>::LOADS], const float* __restrict__ p,
+                                  int64_t srow, int64_t sk, uint32_t rows_left, uint32_t k0,
+                                  uint32_t klen, int tid) {
+#pragma unroll
+    for (int i = 0; i < Geo<BK>::LOADS; ++i) {
+        const int idx = i * GEMM_THREADS + tid;
+        if constexpr (MODE == LOAD_MN) {
+            const uint32_t kr = k0 + idx / (BM / 4);
+            const uint32_t row = (idx % (BM / 4)) * 4;
+            const float* q = p + static_cast<int64_t>(kr) * sk + row;
+            if (FULL || (kr < klen && row + 4 <= rows_left)) {
+                r[i] = *reinterpret_cast<const floatx4*>(q);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[i][e] = (kr < klen && row + e < rows_left) ? q[e] : 0.0f;
+            }
+        } else {
+            const uint32_t row = idx / (BK / 4);
+            const uint32_t kk = k0 + (idx % (BK / 4)) * 4;
+            if constexpr (MODE == LOAD_K) {
+                const float* q = p + static_cast<int64_t>(row) * srow + kk;
+                if (FULL || (row < rows_left && kk + 4 <= klen)) {
+                    r[i] = *reinterpret_cast<const floatx4*>(q);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[i][e] = (row < rows_left && kk + e < klen) ? q[e] : 0.0f;
+                }
+            } else {
+                const float* q = p + static_cast<int64_t>(row) * srow;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    r[i][e] = (FULL || (row < rows_left && kk + e < klen))
+                                  ? q[static_cast<int64_t>(kk + e) * sk]
+                                  : 0.0f;
+                }
+            }
+        }
+    }
+}
+
+template <int MODE, int BK>
+__device__ inline void store_slice(float* __restrict__ st, const floatx4 (&r)[Geo<BK>::LOADS],
+                                   int tid) {
+#pragma unroll
+    for (int i = 0; i < Geo<BK>::LOADS; ++i) {
+        const int idx = i * GEMM_THREADS + tid;
+        if constexpr (MODE == LOAD_MN) {
+            const int kr = idx / (BM / 4), row = (idx % (BM / 4)) * 4;
+            *reinterpret_cast<floatx4*>(st + kr * PMN + row) = r[i];
+        } else {
+            const int row = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
+            *reinterpret_cast<floatx4*>(st + row * Geo<BK>::PK + kq) = r[i];
+        }
+    }
+}
+
+// Operand values of the two 32-row blocks `base_row + {0, 32}` for MFMA steps 4g..4g+3.
+template <int MODE, int BK>
+__device__ inline void read_frag(floatx4 (&v)[2], const float* __restrict__ st, int base_row,
+                                 int g, int lr, int h) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = base_row + i * 32 + lr;
+        if constexpr (MODE == LOAD_MN) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) v[i][s] = st[(g * 8 + h * 4 + s) * PMN + row];
+        } else {
+            v[i] = *reinterpret_cast<const floatx4*>(st + row * Geo<BK>::PK + g * 8 + h * 4);
+        }
+    }
+}
+
+__device__ inline void mfma_group(floatx16 (&acc)[2][2], const floatx4 (&av)[2],
+                                  const floatx4 (&bv)[2]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j],
+                                                                 0, 0, 0);
+}
+
+template <int AM, int BMD, int BK, bool PIPE>
+__global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
+    using G = Geo<BK>;
+    constexpr int A_ST = G::template stage<AM>();
+    constexpr int B_ST = G::template stage<BMD>();
+    constexpr int GROUPS = BK / 8;
+    __shared__ __attribute__((aligned(16))) float smem[2 * (A_ST + B_ST)];
+    float* As = smem;
+    float* Bs = smem + 2 * A_ST;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, h = lane >> 5;
+
+    uint32_t plane, tm, tn;
+    decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t kb = split * p.k_chunk;
+    const uint32_t klen = min(p.k - kb, p.k_chunk);
+    const uint32_t mrem = p.m - m0, nrem = p.n - n0;
+
+    const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
+                     static_cast<int64_t>(kb) * p.a_sk;
+    const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
+                     static_cast<int64_t>(kb) * p.b_sk;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    floatx4 ra[G::LOADS], rb[G::LOADS];
+    const uint32_t ktiles = (klen + BK - 1) / BK;
+    // Workgroup-uniform: the tile's M x N window lies inside the operands, so a K-slice is
+    // "full" whenever its k range is.
+    const bool inner = mrem >= BM && nrem >= BN;
+    auto load = [&](uint32_t k0) {
+        if (inner && k0 + BK <= klen) {
+            load_slice<AM, true, BK>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
+            load_slice<BMD, true, BK>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
+        } else {
+            load_slice<AM, false, BK>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
+            load_slice<BMD, false, BK>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
+        }
+    };
+    load(0);
+    store_slice<AM, BK>(As, ra, tid);
+    store_slice<BMD, BK>(Bs, rb, tid);
+    __syncthreads();
+
+    for (uint32_t kt = 0; kt < ktiles; ++kt) {
+        const int s = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) load((kt + 1) * BK);
+        const float* as = As + s * A_ST;
+        const float* bs = Bs + s * B_ST;
+        if constexpr (PIPE) {
+            floatx4 fa[2][2], fb[2][2];
+            read_frag<AM, BK>(fa[0], as, wm * 64, 0, lr, h);
+            read_frag<BMD, BK>(fb[0], bs, wn * 64, 0, lr, h);
+#pragma unroll
+            for (int g = 0; g < GROUPS; ++g) {
+                if (g + 1 < GROUPS) {
+                    read_frag<AM, BK>(fa[(g + 1) & 1], as, wm * 64, g + 1, lr, h);
+                    read_frag<BMD, BK>(fb[(g + 1) & 1], bs, wn * 64, g + 1, lr, h);
+                }
+                mfma_group(acc, fa[g & 1], fb[g & 1]);
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < GROUPS; ++g) {
+                floatx4 av[2], bv[2];
+                read_frag<AM, BK>(av, as, wm * 64, g, lr, h);
+                read_frag<BMD, BK>(bv, bs, wn * 64, g, lr, h);
+                mfma_group(acc, av, bv);
+            }
+        }
+        if (more) {
+            store_slice<AM, BK>(As + (s ^ 1) * A_ST, ra, tid);
+            store_slice<BMD, BK>(Bs + (s ^ 1) * B_ST, rb, tid);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue. Accumulator register r of block (i, j) holds
+    // row = 8*(r/4) + 4*h + r%4, col = lane%32 of that 32x32 block.
+    if (p.partial != nullptr) {
+        float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                    const uint32_t col = n0 + wn * 64 + j * 32 + lr;
+                    if (inner || (row < p.m && col < p.n)) {
+                        P[static_cast<int64_t>(row) * p.n + col] = acc[i][j][r];
+                    }
+                }
+        return;
+    }
+    float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                const uint32_t col = n0 + wn * 64 + j * 32 + lr;
+                if (inner || (row < p.m && col < p.n)) {
+                    float* q = C + static_cast<int64_t>(row) * p.c_sm +
+                               static_cast<int64_t>(col) * p.c_sn;
+                    float v = p.alpha * acc[i][j][r];
+                    if (p.beta != 0.0f) v = v + p.beta * *q;
+                    *q = v;
+                }
+            }
+}
+
+}  // namespace gemm_detail
+}  // namespace lg

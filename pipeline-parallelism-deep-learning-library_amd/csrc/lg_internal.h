@@ -94,7 +94,8 @@ enum LoadMode : int { LOAD_K = 0, LOAD_MN = 1, LOAD_S = 2 };
 // Tile geometry of the MFMA GEMM kernel.
 constexpr uint32_t GEMM_BM = 128;
 constexpr uint32_t GEMM_BN = 128;
-constexpr uint32_t GEMM_BK = 32;
+constexpr uint32_t GEMM_BK = 16;       // K-slice depth per LDS stage
+constexpr bool GEMM_PIPE = true;       // double-buffer LDS fragments across MFMA groups
 constexpr uint32_t GEMM_THREADS = 256;
 
 struct GemmArgs {
@@ -152,7 +153,8 @@ uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits
 // Permutation kernels
 // ---------------------------------------------------------------------------------------
 constexpr uint32_t PERM_MAX_RANK = 8;  // MAX_RANK, src/ops/permutation.rs:14-16
-constexpr uint32_t PERM_TILE = 64;     // edge of the LDS transpose tile, in elements
+constexpr uint32_t PERM_TILE_A = 64;   // transpose tile extent along a (source unit stride)
+constexpr uint32_t PERM_TILE_B = 64;   // transpose tile extent along b (destination unit stride)
 constexpr uint32_t PERM_THREADS = 256;
 
 struct PermTileArgs {

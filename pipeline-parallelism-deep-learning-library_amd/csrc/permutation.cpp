@@ -214,8 +214,8 @@ Gather plan_gather(lg_elem elem, const View& src, const View& dst, bool conj_req
         ++o;
     }
     p.outer_rank = o;
-    p.tiles_a = static_cast<uint32_t>((shape[a] + PERM_TILE - 1) / PERM_TILE);
-    p.tiles_b = static_cast<uint32_t>((shape[b] + PERM_TILE - 1) / PERM_TILE);
+    p.tiles_a = static_cast<uint32_t>((shape[a] + PERM_TILE_A - 1) / PERM_TILE_A);
+    p.tiles_b = static_cast<uint32_t>((shape[b] + PERM_TILE_B - 1) / PERM_TILE_B);
     p.total_tiles = static_cast<uint64_t>(p.tiles_a) * p.tiles_b * outer_count;
     g.info.vector = vec ? 1 : 0;
     g.info.workgroups = perm_tile_workgroups(p.total_tiles);
