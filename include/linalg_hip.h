@@ -240,6 +240,8 @@ typedef struct lg_permute_plan {
     uint32_t axis_b;        /* tile: destination unit-stride axis (rank - 1) */
     uint32_t vector;        /* 1 when the 128-bit path is legal (alignment) */
     uint32_t conj;          /* 1 when the imaginary sign bit is flipped */
+    uint32_t streaming;     /* 1 when accesses are non-temporal (operands exceed the cache) */
+    uint32_t reserved;
     uint64_t shape[8];      /* coalesced extents */
     uint64_t strides[8];    /* coalesced source strides */
     uint64_t workgroups;    /* workgroups of the launch */

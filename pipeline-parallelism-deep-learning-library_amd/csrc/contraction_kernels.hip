@@ -12,23 +12,72 @@ namespace {
 
 using gemm_detail::gemm_f32_mfma;
 
-// Split-K second pass: for every output, sum the partials of splits 0..S-1 in order, then
-// apply alpha and beta once. Partials are [batch][splits][m][n], dense.
-__global__ __launch_bounds__(256) void reduce_f32(ReduceArgs p) {
+// Split-K second pass. Partials are [batch][splits][m][n], dense. A workgroup owns 64 runs
+// of V consecutive outputs; its four waves each sum a fixed quarter of the splits in
+// ascending order (8 loads in flight), the quarters are added in order 0+1+2+3, and alpha and
+// beta are applied once. The order depends only on the split count, so results are
+// bit-reproducible from run to run. V = 4 (128-bit loads) whenever n is a multiple of 4.
+constexpr int RED_LANES = 64;
+constexpr int RED_SLICES = 4;
+
+template <int V>
+__global__ __launch_bounds__(RED_LANES * RED_SLICES) void reduce_f32(ReduceArgs p) {
+    typedef float vec __attribute__((ext_vector_type(4)));
+    __shared__ vec part[RED_SLICES][RED_LANES];
+    const int lane = threadIdx.x % RED_LANES, q = threadIdx.x / RED_LANES;
     const uint64_t mn = static_cast<uint64_t>(p.m) * p.n;
     const uint64_t count = mn * p.batch;
-    for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < count;
-         e += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-        const uint64_t bi = e / mn, rem = e - bi * mn;
-        const uint32_t row = static_cast<uint32_t>(rem / p.n), col = static_cast<uint32_t>(rem % p.n);
-        const float* src = p.partial + bi * p.splits * mn + rem;
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < p.splits; ++s) acc = acc + src[s * mn];
-        float* q = p.c + static_cast<int64_t>(bi) * p.c_sb + static_cast<int64_t>(row) * p.c_sm +
-                   static_cast<int64_t>(col) * p.c_sn;
-        float v = p.alpha * acc;
-        if (p.beta != 0.0f) v = v + p.beta * *q;
-        *q = v;
+    const uint32_t s0 = static_cast<uint32_t>(static_cast<uint64_t>(q) * p.splits / RED_SLICES);
+    const uint32_t s1 = static_cast<uint32_t>(static_cast<uint64_t>(q + 1) * p.splits / RED_SLICES);
+    const uint64_t step = static_cast<uint64_t>(gridDim.x) * RED_LANES * V;
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * RED_LANES * V; base < count; base += step) {
+        const uint64_t e = base + static_cast<uint64_t>(lane) * V;
+        vec acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        uint64_t bi = 0, rem = 0;
+        if (e < count) {
+            bi = e / mn;
+            rem = e - bi * mn;
+            const float* src = p.partial + bi * p.splits * mn + rem;
+            uint32_t s = s0;
+            for (; s + 8 <= s1; s += 8) {
+                vec x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if constexpr (V == 4) {
+                        x[u] = *reinterpret_cast<const vec*>(src + (s + u) * mn);
+                    } else {
+                        x[u][0] = src[(s + u) * mn];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = acc + x[u];
+            }
+            for (; s < s1; ++s) {
+                if constexpr (V == 4) {
+                    acc = acc + *reinterpret_cast<const vec*>(src + s * mn);
+                } else {
+                    acc[0] = acc[0] + src[s * mn];
+                }
+            }
+        }
+        part[q][lane] = acc;
+        __syncthreads();
+        if (q == 0 && e < count) {
+            vec t = part[0][lane];
+#pragma unroll
+            for (int k = 1; k < RED_SLICES; ++k) t = t + part[k][lane];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                const uint64_t r = rem + v;
+                const uint32_t row = static_cast<uint32_t>(r / p.n), col = static_cast<uint32_t>(r % p.n);
+                float* out = p.c + static_cast<int64_t>(bi) * p.c_sb + static_cast<int64_t>(row) * p.c_sm +
+                             static_cast<int64_t>(col) * p.c_sn;
+                float val = p.alpha * t[v];
+                if (p.beta != 0.0f) val = val + p.beta * *out;
+                *out = val;
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -136,7 +185,15 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
 
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args) {
     const uint64_t count = static_cast<uint64_t>(args.m) * args.n * args.batch;
-    hipLaunchKernelGGL(reduce_f32, dim3(grid_for(count)), dim3(256), 0, s, args);
+    const int v = args.n % 4 == 0 ? 4 : 1;
+    const uint64_t per = static_cast<uint64_t>(RED_LANES) * v;
+    const uint64_t g = (count + per - 1) / per;
+    const dim3 grid(static_cast<uint32_t>(g < 65536 ? (g ? g : 1) : 65536));
+    if (v == 4) {
+        hipLaunchKernelGGL(reduce_f32<4>, grid, dim3(RED_LANES * RED_SLICES), 0, s, args);
+    } else {
+        hipLaunchKernelGGL(reduce_f32<1>, grid, dim3(RED_LANES * RED_SLICES), 0, s, args);
+    }
     check_launch("reduce_f32 launch");
     note_launch(ctx, "reduce_f32");
 }

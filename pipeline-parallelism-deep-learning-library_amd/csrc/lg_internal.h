@@ -155,6 +155,11 @@ uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits
 constexpr uint32_t PERM_MAX_RANK = 8;  // MAX_RANK, src/ops/permutation.rs:14-16
 constexpr uint32_t PERM_TILE_A = 64;   // transpose tile extent along a (source unit stride)
 constexpr uint32_t PERM_TILE_B = 64;   // transpose tile extent along b (destination unit stride)
+// Streaming configuration, used when source + destination exceed the 256 MiB Infinity Cache
+// (nothing of the operands survives in cache between uses, so accesses are non-temporal and
+// tiles are twice as long along the source rows).
+constexpr uint32_t PERM_STREAM_TILE_A = 128;
+constexpr uint64_t PERM_STREAM_BYTES = 256ull << 20;
 constexpr uint32_t PERM_THREADS = 256;
 
 struct PermTileArgs {
@@ -178,13 +183,14 @@ struct PermCopyArgs {
     uint32_t rank;
     uint32_t contiguous;  // rank 1, unit stride, aligned: straight vector copy
     uint32_t vec_dst;     // destination offset aligned for 128-bit stores
+    uint32_t streaming;   // non-temporal 128-bit accesses
     uint64_t shape[PERM_MAX_RANK];
     int64_t strides[PERM_MAX_RANK];
 };
 
 // words: 1 (4-byte elements) or 2 (8-byte complex); conj flips the imaginary sign bit.
 void launch_perm_tile(Context* ctx, hipStream_t s, const PermTileArgs& args, int words, bool conj,
-                      bool vec);
+                      bool vec, bool streaming);
 void launch_perm_copy(Context* ctx, hipStream_t s, const PermCopyArgs& args, int words, bool conj);
 uint64_t perm_copy_workgroups(uint64_t count, int words);
 uint64_t perm_tile_workgroups(uint64_t total_tiles);

@@ -181,7 +181,9 @@ Gather plan_gather(lg_elem elem, const View& src, const View& dst, bool conj_req
         p.vec_dst = (dst.base % 16 == 0 && dst.offset % ve == 0) ? 1 : 0;
         p.contiguous = (rank == 1 && strides[0] == 1 && src.base % 16 == 0 &&
                         src.offset % ve == 0 && p.vec_dst) ? 1 : 0;
+        p.streaming = (p.contiguous && 2 * p.count * e.bytes > PERM_STREAM_BYTES) ? 1 : 0;
         g.info.vector = p.contiguous;
+        g.info.streaming = p.streaming;
         g.info.workgroups = perm_copy_workgroups(p.count, e.words);
         return g;
     }
@@ -214,7 +216,10 @@ Gather plan_gather(lg_elem elem, const View& src, const View& dst, bool conj_req
         ++o;
     }
     p.outer_rank = o;
-    p.tiles_a = static_cast<uint32_t>((shape[a] + PERM_TILE_A - 1) / PERM_TILE_A);
+    const uint64_t moved = 2 * dst.len() * e.bytes;
+    g.info.streaming = (vec && moved > PERM_STREAM_BYTES) ? 1 : 0;
+    const uint32_t tile_a = g.info.streaming ? PERM_STREAM_TILE_A : PERM_TILE_A;
+    p.tiles_a = static_cast<uint32_t>((shape[a] + tile_a - 1) / tile_a);
     p.tiles_b = static_cast<uint32_t>((shape[b] + PERM_TILE_B - 1) / PERM_TILE_B);
     p.total_tiles = static_cast<uint64_t>(p.tiles_a) * p.tiles_b * outer_count;
     g.info.vector = vec ? 1 : 0;
@@ -250,7 +255,8 @@ void run(lg_ctx* ctx, void* stream, uint32_t op, lg_elem elem, const lg_view* sr
     set_device(ctx);
     hipStream_t s = pick_stream(ctx, stream);
     if (g.info.kind == LG_PERMUTE_TILE) {
-        launch_perm_tile(ctx, s, g.tile, g.words, g.conj, g.info.vector != 0);
+        launch_perm_tile(ctx, s, g.tile, g.words, g.conj, g.info.vector != 0,
+                         g.info.streaming != 0);
     } else {
         launch_perm_copy(ctx, s, g.copy, g.words, g.conj);
     }

@@ -16,7 +16,7 @@ using perm_detail::perm_tile;
 using perm_detail::SIGN;
 using perm_detail::u32x4;
 
-template <int W, bool CONJ>
+template <int W, bool CONJ, bool NT>
 __global__ __launch_bounds__(PERM_THREADS) void perm_copy(PermCopyArgs p) {
     constexpr int VE = 4 / W;
     const uint32_t* src = static_cast<const uint32_t*>(p.src);
@@ -30,7 +30,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_copy(PermCopyArgs p) {
         if (p.contiguous) {
             const uint64_t s0 = p.src_offset + i0;
             if (full) {
-                v = *reinterpret_cast<const u32x4*>(src + s0 * W);
+                v = perm_detail::load128<NT>(src + s0 * W);
             } else {
                 for (int e = 0; e < VE; ++e)
                     if (i0 + e < p.count)
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_copy(PermCopyArgs p) {
         }
         const uint64_t d0 = p.dst_offset + i0;
         if (full && p.vec_dst) {
-            *reinterpret_cast<u32x4*>(dst + d0 * W) = v;
+            perm_detail::store128<NT>(dst + d0 * W, v);
         } else {
             for (int e = 0; e < VE; ++e)
                 if (i0 + e < p.count)
@@ -75,12 +75,17 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_copy(PermCopyArgs p) {
 constexpr uint64_t TILE_GRID_CAP = 1u << 22;
 constexpr uint64_t COPY_GRID_CAP = 1u << 20;
 
-template <int W, bool CONJ, bool VEC>
+template <int W, bool CONJ, bool VEC, int TA, bool NT>
 void tile_t(hipStream_t s, const PermTileArgs& a) {
     const uint64_t g = perm_tile_workgroups(a.total_tiles);
-    hipLaunchKernelGGL((perm_tile<W, CONJ, VEC, PERM_TILE_A, PERM_TILE_B>),
-                       dim3(static_cast<uint32_t>(g)),
-                       dim3(PERM_THREADS), 0, s, a);
+    hipLaunchKernelGGL((perm_tile<W, CONJ, VEC, TA, PERM_TILE_B, NT>),
+                       dim3(static_cast<uint32_t>(g)), dim3(PERM_THREADS), 0, s, a);
+}
+
+template <int W, bool CONJ, bool NT>
+void copy_t(hipStream_t s, const PermCopyArgs& a) {
+    const dim3 grid(static_cast<uint32_t>(perm_copy_workgroups(a.count, W)));
+    hipLaunchKernelGGL((perm_copy<W, CONJ, NT>), grid, dim3(PERM_THREADS), 0, s, a);
 }
 
 }  // namespace
@@ -96,34 +101,38 @@ uint64_t perm_copy_workgroups(uint64_t count, int words) {
 }
 
 void launch_perm_tile(Context* ctx, hipStream_t s, const PermTileArgs& a, int words, bool conj,
-                      bool vec) {
+                      bool vec, bool streaming) {
+    constexpr int TS = PERM_STREAM_TILE_A, TN = PERM_TILE_A;
     const char* name = nullptr;
     if (words == 1) {
-        if (vec) tile_t<1, false, true>(s, a), name = "perm_tile_w1_v128";
-        else tile_t<1, false, false>(s, a), name = "perm_tile_w1";
+        if (streaming) tile_t<1, false, true, TS, true>(s, a), name = "perm_tile_w1_v128_stream";
+        else if (vec) tile_t<1, false, true, TN, false>(s, a), name = "perm_tile_w1_v128";
+        else tile_t<1, false, false, TN, false>(s, a), name = "perm_tile_w1";
     } else if (!conj) {
-        if (vec) tile_t<2, false, true>(s, a), name = "perm_tile_w2_v128";
-        else tile_t<2, false, false>(s, a), name = "perm_tile_w2";
+        if (streaming) tile_t<2, false, true, TS, true>(s, a), name = "perm_tile_w2_v128_stream";
+        else if (vec) tile_t<2, false, true, TN, false>(s, a), name = "perm_tile_w2_v128";
+        else tile_t<2, false, false, TN, false>(s, a), name = "perm_tile_w2";
     } else {
-        if (vec) tile_t<2, true, true>(s, a), name = "perm_tile_conj_w2_v128";
-        else tile_t<2, true, false>(s, a), name = "perm_tile_conj_w2";
+        if (streaming) tile_t<2, true, true, TS, true>(s, a), name = "perm_tile_conj_w2_v128_stream";
+        else if (vec) tile_t<2, true, true, TN, false>(s, a), name = "perm_tile_conj_w2_v128";
+        else tile_t<2, true, false, TN, false>(s, a), name = "perm_tile_conj_w2";
     }
     check_hip(hipGetLastError(), "perm_tile launch");
     note_launch(ctx, name);
 }
 
 void launch_perm_copy(Context* ctx, hipStream_t s, const PermCopyArgs& a, int words, bool conj) {
-    const dim3 grid(static_cast<uint32_t>(perm_copy_workgroups(a.count, words)));
+    const bool nt = a.streaming != 0;
     const char* name;
     if (words == 1) {
-        hipLaunchKernelGGL((perm_copy<1, false>), grid, dim3(PERM_THREADS), 0, s, a);
-        name = "perm_copy_w1";
+        if (nt) copy_t<1, false, true>(s, a), name = "perm_copy_w1_stream";
+        else copy_t<1, false, false>(s, a), name = "perm_copy_w1";
     } else if (!conj) {
-        hipLaunchKernelGGL((perm_copy<2, false>), grid, dim3(PERM_THREADS), 0, s, a);
-        name = "perm_copy_w2";
+        if (nt) copy_t<2, false, true>(s, a), name = "perm_copy_w2_stream";
+        else copy_t<2, false, false>(s, a), name = "perm_copy_w2";
     } else {
-        hipLaunchKernelGGL((perm_copy<2, true>), grid, dim3(PERM_THREADS), 0, s, a);
-        name = "perm_copy_conj_w2";
+        if (nt) copy_t<2, true, true>(s, a), name = "perm_copy_conj_w2_stream";
+        else copy_t<2, true, false>(s, a), name = "perm_copy_conj_w2";
     }
     check_hip(hipGetLastError(), "perm_copy launch");
     note_launch(ctx, name);

@@ -23,7 +23,19 @@ namespace perm_detail {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t SIGN = 0x80000000u;
 
-template <int W, bool CONJ, bool VEC, int TA, int TB>
+// 128-bit global accesses; NT marks them non-temporal (streamed past the caches).
+template <bool NT>
+__device__ inline u32x4 load128(const uint32_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    else return *reinterpret_cast<const u32x4*>(p);
+}
+template <bool NT>
+__device__ inline void store128(uint32_t* p, u32x4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+    else *reinterpret_cast<u32x4*>(p) = v;
+}
+
+template <int W, bool CONJ, bool VEC, int TA, int TB, bool NT = false>
 __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
     constexpr int VE = 4 / W;                       // elements per 128-bit word
     constexpr int PITCH = TA * W + 1;               // LDS row pitch in words (rows are b)
@@ -65,7 +77,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             uint32_t* row = tile + bb * PITCH + cw;
             const int64_t e0 = sbase + static_cast<int64_t>(b) * p.src_sb + a;  // element index
             if (VEC && b < p.ext_b && a + VE <= p.ext_a) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(src + e0 * W);
+                const u32x4 v = load128<NT>(src + e0 * W);
                 row[0] = v[0];
                 row[1] = v[1];
                 row[2] = v[2];
@@ -101,7 +113,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             }
             const int64_t e0 = dbase + static_cast<int64_t>(a) * p.dst_sa + b;
             if (VEC && a < p.ext_a && b + VE <= p.ext_b) {
-                *reinterpret_cast<u32x4*>(dst + e0 * W) = v;
+                store128<NT>(dst + e0 * W, v);
             } else {
 #pragma unroll
                 for (int e = 0; e < VE; ++e) {
@@ -113,6 +125,129 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             }
         }
         __syncthreads();
+    }
+}
+
+
+// Software-pipelined variant for views that allow 128-bit accesses: each workgroup walks
+// several tiles and, after staging tile t in LDS, issues the HBM reads of its next tile before
+// draining tile t, so the read and write streams of one workgroup overlap.
+template <int W, bool CONJ, int TA, int TB, bool NT>
+__global__ __launch_bounds__(PERM_THREADS) void perm_tile_pipe(PermTileArgs p) {
+    constexpr int VE = 4 / W;
+    constexpr int PITCH = TA * W + 1;
+    constexpr int FILL_CHUNKS = TA * W / 4;
+    constexpr int DRAIN_CHUNKS = TB * W / 4;
+    constexpr int FILL_ITERS = TB * FILL_CHUNKS / PERM_THREADS;
+    constexpr int DRAIN_ITERS = TA * DRAIN_CHUNKS / PERM_THREADS;
+    static_assert(FILL_ITERS * PERM_THREADS == TB * FILL_CHUNKS, "fill must split evenly");
+    static_assert(DRAIN_ITERS * PERM_THREADS == TA * DRAIN_CHUNKS, "drain must split evenly");
+    __shared__ uint32_t tile[TB * PITCH];
+
+    const uint32_t* src = static_cast<const uint32_t*>(p.src);
+    uint32_t* dst = static_cast<uint32_t*>(p.dst);
+    const int tid = threadIdx.x;
+    const uint64_t per_outer = static_cast<uint64_t>(p.tiles_a) * p.tiles_b;
+
+    struct Pos {
+        int64_t sbase, dbase;
+        uint32_t a0, b0;
+    };
+    auto locate = [&](uint64_t t) {
+        Pos q;
+        uint64_t outer = t / per_outer;
+        const uint64_t rem = t - outer * per_outer;
+        const uint32_t tb = static_cast<uint32_t>(rem / p.tiles_a);
+        const uint32_t ta = static_cast<uint32_t>(rem - static_cast<uint64_t>(tb) * p.tiles_a);
+        q.sbase = static_cast<int64_t>(p.src_offset);
+        q.dbase = static_cast<int64_t>(p.dst_offset);
+        for (int d = static_cast<int>(p.outer_rank) - 1; d >= 0; --d) {
+            const uint64_t qq = outer / p.outer_shape[d];
+            const int64_t c = static_cast<int64_t>(outer - qq * p.outer_shape[d]);
+            q.sbase += c * p.outer_src[d];
+            q.dbase += c * p.outer_dst[d];
+            outer = qq;
+        }
+        q.a0 = ta * TA;
+        q.b0 = tb * TB;
+        return q;
+    };
+    u32x4 r[FILL_ITERS];
+    auto fetch = [&](const Pos& q) {
+#pragma unroll
+        for (int it = 0; it < FILL_ITERS; ++it) {
+            const int idx = it * PERM_THREADS + tid;
+            const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
+            const uint32_t a = q.a0 + cw / W, b = q.b0 + bb;
+            const int64_t e0 = q.sbase + static_cast<int64_t>(b) * p.src_sb + a;
+            if (b < p.ext_b && a + VE <= p.ext_a) {
+                r[it] = load128<NT>(src + e0 * W);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VE; ++e)
+#pragma unroll
+                    for (int w = 0; w < W; ++w)
+                        r[it][e * W + w] = (b < p.ext_b && a + e < p.ext_a) ? src[(e0 + e) * W + w] : 0u;
+            }
+        }
+    };
+
+    uint64_t t = blockIdx.x;
+    if (t >= p.total_tiles) return;
+    Pos cur = locate(t);
+    fetch(cur);
+    for (;;) {
+#pragma unroll
+        for (int it = 0; it < FILL_ITERS; ++it) {
+            const int idx = it * PERM_THREADS + tid;
+            const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
+            uint32_t* row = tile + bb * PITCH + cw;
+            row[0] = r[it][0];
+            row[1] = r[it][1];
+            row[2] = r[it][2];
+            row[3] = r[it][3];
+        }
+        __syncthreads();
+        const uint64_t tn = t + gridDim.x;
+        const bool more = tn < p.total_tiles;
+        Pos next = cur;
+        if (more) {
+            next = locate(tn);
+            fetch(next);
+        }
+#pragma unroll
+        for (int it = 0; it < DRAIN_ITERS; ++it) {
+            const int idx = it * PERM_THREADS + tid;
+            const int aa = idx / DRAIN_CHUNKS, cw = (idx % DRAIN_CHUNKS) * 4;
+            const int bl = cw / W;
+            const uint32_t a = cur.a0 + aa, b = cur.b0 + bl;
+            u32x4 v;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) {
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    uint32_t word = tile[(bl + e) * PITCH + aa * W + w];
+                    if (CONJ && w == 1) word ^= SIGN;
+                    v[e * W + w] = word;
+                }
+            }
+            const int64_t e0 = cur.dbase + static_cast<int64_t>(a) * p.dst_sa + b;
+            if (a < p.ext_a && b + VE <= p.ext_b) {
+                store128<NT>(dst + e0 * W, v);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VE; ++e) {
+                    if (a < p.ext_a && b + e < p.ext_b) {
+#pragma unroll
+                        for (int w = 0; w < W; ++w) dst[(e0 + e) * W + w] = v[e * W + w];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (!more) break;
+        t = tn;
+        cur = next;
     }
 }
 

@@ -37,7 +37,8 @@ class lg_contract_plan(ctypes.Structure):
 
 class lg_permute_plan(ctypes.Structure):
     _fields_ = [("kind", u32), ("rank", u32), ("axis_a", u32), ("axis_b", u32), ("vector", u32),
-                ("conj", u32), ("shape", u64 * 8), ("strides", u64 * 8), ("workgroups", u64)]
+                ("conj", u32), ("streaming", u32), ("reserved", u32), ("shape", u64 * 8),
+                ("strides", u64 * 8), ("workgroups", u64)]
 
 
 VP = ctypes.POINTER(lg_view)

@@ -82,5 +82,6 @@ def plan(op: str, src: TensorView, dst: TensorView) -> dict:
                                   ctypes.byref(dst.to_c()), ctypes.byref(out)))
     return {"kind": N.PERMUTE_KINDS[out.kind], "rank": out.rank, "axis_a": out.axis_a,
             "axis_b": out.axis_b, "vector": bool(out.vector), "conj": bool(out.conj),
+            "streaming": bool(out.streaming),
             "shape": list(out.shape[:out.rank]), "strides": list(out.strides[:out.rank]),
             "workgroups": out.workgroups}

@@ -129,11 +129,13 @@ def test_permutation_plans_for_the_baseline_configs():
     p = P.plan("materialize", P.permute_view(x, [2, 0, 1]), y)
     assert p["kind"] == "tile" and p["shape"] == [256, 524288] and p["strides"] == [1, 256]
     assert (p["axis_a"], p["axis_b"], p["vector"]) == (0, 1, True)
+    assert p["streaming"] and p["workgroups"] == 2 * 8192  # 1 GiB moved: 128 x 64 streaming tiles
     x = view(Layout.dense([64, 128, 64, 32]))
     y = view(Layout.dense([64, 64, 32, 128]))
     p = P.plan("materialize", P.permute_view(x, [0, 2, 3, 1]), y)
     assert p["kind"] == "tile" and p["shape"] == [64, 2048, 128]
     assert p["strides"] == [262144, 1, 2048] and p["axis_a"] == 1 and p["vector"]
+    assert not p["streaming"] and p["workgroups"] == 64 * 32 * 2  # 128 MiB moved: cached tiles
 
 
 def test_permutation_path_choice_and_coalescing():
