@@ -162,7 +162,7 @@ def cpu_baselines(gemm_host, perm_host, args):
     a, b = gemm_host
     n = 4096
     # Literal single-thread accumulation (what crates/cpu runs): a sample of output rows.
-    rows = np.arange(2, dtype=np.uint64)
+    rows = np.arange(48, dtype=np.uint64)
     c = np.zeros(n * n, np.float32)
     t0 = time.perf_counter()
     for r in rows:
@@ -173,7 +173,7 @@ def cpu_baselines(gemm_host, perm_host, args):
                        "sample": f"{len(rows)} of 4096 output rows of the 4096^3 gemm, "
                                  f"literal k-order loop ({dt:.1f} s)"}
     threads = min(os.cpu_count() or 1, 16)
-    rows = np.arange(128, dtype=np.uint64)
+    rows = np.arange(n, dtype=np.uint64)
     t0 = time.perf_counter()
     oracle.gemm_fast(n, n, n, 1.0, 0.0, a, 0, (n, 1), b, 0, (n, 1), c, 0, (n, 1), rows=rows,
                      threads=threads)
@@ -181,20 +181,20 @@ def cpu_baselines(gemm_host, perm_host, args):
     flops = 2.0 * len(rows) * n * n
     out["gemm_fast"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
                         "kind": "port",
-                        "sample": f"{len(rows)} of 4096 output rows, bit-identical loop-interchanged "
-                                  f"variant on {threads} threads ({dt:.1f} s)"}
+                         "sample": f"all {len(rows)} output rows of the 4096^3 gemm, bit-identical "
+                                  f"loop-interchanged variant on {threads} threads ({dt:.1f} s)"}
     x = perm_host
     shape, perm = [512, 1024, 256], [2, 0, 1]
-    # gather_words over the first 32 of 256 output planes (dst[c] = src[:, :, c]).
-    sample_planes = 32
+    # gather_words over all 256 output planes (dst[c] = src[:, :, c]).
+    sample_planes = 256
     t0 = time.perf_counter()
     words = x.view(np.uint32)
     oracle.gather_words(words, 1, 0, [sample_planes, 512, 1024], [1, 1024 * 256, 256])
     dt = time.perf_counter() - t0
     nbytes = 2.0 * sample_planes * 512 * 1024 * 4
     out["permute"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                      "sample": f"gather_words of {sample_planes} of 256 output planes of "
-                                f"[512,1024,256] perm (2,0,1) ({dt:.1f} s)"}
+                      "sample": f"gather_words of all {sample_planes} output planes of "
+                                f"[512,1024,256] perm (2,0,1), 1 GiB moved ({dt:.1f} s)"}
     return out
 
 
@@ -298,7 +298,8 @@ def main() -> int:
                             "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                             "frac": round(head["frac"], 4),
                             "traffic": traffic_from_profile("gemm4096"),
-                            "kernel": "gemm_f32_mfma<K,MN>",
+                            "kernel": "gemm_f32_mfma<0, 1, 16, true> (A K-contiguous, B N-contiguous)",
+                            "profile": "profiles/gemm_f32_mfma_gemm4096.md, profiles/traffic_gemm4096.txt",
                             "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
     if cpu:
         line["cpu_baseline"] = cpu["gemm_seq"]
@@ -310,7 +311,8 @@ def main() -> int:
                                         "peak": PEAK_GBS, "unit": "GB/s",
                                         "frac": round(perm["frac"], 4),
                                         "traffic": traffic_from_profile("c2b"),
-                                        "kernel": "perm_tile_w1_v128",
+                                        "kernel": "perm_tile<1, false, true, 128, 64, true> (streaming)",
+                                        "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
                                         "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
                            "cpu_baseline": cpu["permute"] if cpu else None}
     line["configs"] = {k_: {kk: (round(v, 4) if isinstance(v, float) else v)
