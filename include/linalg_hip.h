@@ -186,6 +186,55 @@ lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const l
                              float beta, const lg_view* c);
 
 /* ---------------------------------------------------------------------------------------
+ * Backend-style gemm: linalg_core::Backend::gemm (crates/core/src/lib.rs:143-164)
+ * ------------------------------------------------------------------------------------- */
+
+/* core::Error (crates/core/src/lib.rs:43-53). */
+typedef enum lg_core_error {
+    LG_CORE_OK = 0,
+    LG_CORE_SHAPE = 1,
+    LG_CORE_DTYPE = 2,
+    LG_CORE_UNSUPPORTED_LAYOUT = 3,
+    LG_CORE_UNSUPPORTED_DEVICE = 4,
+    LG_CORE_ALIAS = 5,
+    LG_CORE_TRANSPORT = 6,
+    LG_CORE_WIRE = 7,
+    LG_CORE_SCHEDULE = 8
+} lg_core_error;
+
+/* DType wire tags (crates/core/src/lib.rs:18-24). */
+typedef enum lg_dtype { LG_DTYPE_F32 = 1, LG_DTYPE_F16 = 2, LG_DTYPE_BF16 = 3 } lg_dtype;
+
+/* core::Tensor<S> (crates/core/src/lib.rs:55-61): one storage allocation (its base pointer is
+ * the storage id) plus dtype, shape, strides and offset in elements. */
+typedef struct lg_tensor {
+    void* base;                      /* storage allocation base (device memory) */
+    uint64_t bytes;                  /* storage length in bytes */
+    uint32_t dtype;                  /* lg_dtype */
+    uint32_t rank;                   /* entries of `shape` */
+    uint32_t nstrides;               /* entries of `strides` */
+    uint32_t reserved;
+    uint64_t offset;                 /* in elements */
+    uint64_t shape[LG_MAX_RANK];
+    uint64_t strides[LG_MAX_RANK];
+} lg_tensor;
+
+/* Backend::gemm as CpuBackend::gemm checks it (crates/cpu/src/lib.rs:203-295): `a` is [M, K],
+ * `b` [K, N], `c` [M, N]; a dtype tag outside lg_dtype is LG_CORE_WIRE (DType::from_tag,
+ * crates/core/src/lib.rs:25-32); then checks in order Shape (rank 2, inner extents), Dtype
+ * (all equal), Alias (distinct storage), UnsupportedLayout (offset 0; all row-major, or A or
+ * B a transpose_matrix of a row-major matrix with C row-major), then Shape again for every
+ * operand that is read reaching past its storage. Stores beta*C + alpha*A*B (beta = 0 does
+ * not read C, alpha = 0 does not read A or B, K = 0 with beta = 0 stores zeros); every
+ * product is (alpha*a)*b, as in the reference's loop, summed in the kernel's fixed order.
+ * f32 only: F16 and BF16 return LG_CORE_UNSUPPORTED_DEVICE. The checks run before `ctx` is
+ * used.
+ * Enqueues on `stream` (NULL = context stream) and returns before the device finishes, as
+ * the GPU backends do (crates/core/src/lib.rs:72-82). On any error nothing is launched. */
+lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_tensor* a, const lg_tensor* b,
+                              const lg_tensor* c, float alpha, float beta);
+
+/* ---------------------------------------------------------------------------------------
  * Plan inspection (host only; no context, no device work). These run the exact
  * validation and planning of the entry points above and report the plan instead of
  * launching it, so the planner is testable without a GPU.

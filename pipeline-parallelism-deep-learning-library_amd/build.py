@@ -23,6 +23,7 @@ ARCH = "gfx950"
 
 SOURCES = [
     "abi.cpp",
+    "backend.cpp",
     "contraction.cpp",
     "permutation.cpp",
     "contraction_kernels.hip",

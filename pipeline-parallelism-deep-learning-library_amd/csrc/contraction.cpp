@@ -13,6 +13,7 @@
 // workgroups on each of 256 CUs, independent of the device so results are reproducible
 // across boxes), the operand load modes, and 64-bit addressing (no u32 index limit).
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <unordered_set>
 
@@ -461,7 +462,10 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     const float* bptr = reinterpret_cast<const float*>(b.base) + b.offset;
     const bool single = mg.batch.size() == 1 && mg.m.size() == 1 && mg.n.size() == 1 &&
                         mg.k.size() == 1;
-    if (!single) {
+    // The tiled kernel scales A by alpha as it stages it; with a non-finite alpha its zero
+    // padding would become NaN, so such calls take the general kernel, which reads real
+    // elements only.
+    if (!single || !std::isfinite(alpha)) {
         info.kind = LG_PLAN_GENERAL;
         GeneralArgs& g = p.general;
         g.a = aptr;
@@ -536,7 +540,6 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     r.n = n;
     r.batch = batch;
     r.splits = splits;
-    r.alpha = alpha;
     r.beta = beta;
     return p;
 }
@@ -609,6 +612,14 @@ void run(lg_ctx* ctx, void* stream, Plan plan, bool wait) {
 }
 
 }  // namespace
+
+void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
+                        float beta, const View& c) {
+    Plan plan = plan_merged(a, b, c, merge_all(groups_from_gemm(a, b, c)), alpha, beta);
+    set_device(ctx);
+    execute(ctx, s, plan);
+}
+
 }  // namespace lg
 
 using namespace lg;

@@ -1,7 +1,8 @@
 // gfx950 contraction kernels: the fp32 MFMA GEMM (gemm_kernel.h) instantiated at the
 // library's pipeline shape, the split-K reduction (fixed order over splits, so results are
 // bit-reproducible), the mixed-radix general fallback, and the C = 0 / C = beta*C fill.
-// Everything is compiled with -ffp-contract=off: alpha*acc and beta*C round separately.
+// Every product is formed as (alpha * a) * b, the grouping of the reference's sequential loop.
+// Everything is compiled with -ffp-contract=off: products and sums round separately.
 #include <hip/hip_runtime.h>
 
 #include "gemm_kernel.h"
@@ -14,8 +15,9 @@ using gemm_detail::gemm_f32_mfma;
 
 // Split-K second pass. Partials are [batch][splits][m][n], dense. A workgroup owns 64 runs
 // of V consecutive outputs; its four waves each sum a fixed quarter of the splits in
-// ascending order (8 loads in flight), the quarters are added in order 0+1+2+3, and alpha and
-// beta are applied once. The order depends only on the split count, so results are
+// ascending order (8 loads in flight), the quarters are added in order 0+1+2+3, and beta*C
+// is added once (alpha is already inside the partials). The order depends only on the split
+// count, so results are
 // bit-reproducible from run to run. V = 4 (128-bit loads) whenever n is a multiple of 4.
 constexpr int RED_LANES = 64;
 constexpr int RED_SLICES = 4;
@@ -72,8 +74,8 @@ __global__ __launch_bounds__(RED_LANES * RED_SLICES) void reduce_f32(ReduceArgs 
                 const uint32_t row = static_cast<uint32_t>(r / p.n), col = static_cast<uint32_t>(r % p.n);
                 float* out = p.c + static_cast<int64_t>(bi) * p.c_sb + static_cast<int64_t>(row) * p.c_sm +
                              static_cast<int64_t>(col) * p.c_sn;
-                float val = p.alpha * t[v];
-                if (p.beta != 0.0f) val = val + p.beta * *out;
+                float val = t[v];
+                if (p.beta != 0.0f) val = p.beta * *out + val;
                 *out = val;
             }
         }
@@ -93,8 +95,10 @@ __device__ inline int64_t decode4(const Axes4& ax, uint64_t idx) {
     return off;
 }
 
-// Fallback for groups that keep more than one stride after merging: one thread per output,
-// K walked in order with an odometer over the (up to four) K axes of A and B.
+// Fallback for groups that keep more than one stride after merging, and for non-finite alpha:
+// one thread per output, acc = (beta == 0 ? 0 : beta*C), then acc += (alpha*a)*b in k order
+// with an odometer over the (up to four) K axes of A and B -- the reference's sequential
+// loop, so this kernel's results are bit-identical to it.
 __global__ __launch_bounds__(256) void general_f32(GeneralArgs p) {
     const uint64_t mn = static_cast<uint64_t>(p.m) * p.n;
     const uint64_t count = mn * p.batch;
@@ -104,11 +108,12 @@ __global__ __launch_bounds__(256) void general_f32(GeneralArgs p) {
         const uint64_t mi = rem / p.n, ni = rem - mi * p.n;
         const float* a = p.a + decode4(p.a_batch, bi) + decode4(p.a_m, mi);
         const float* b = p.b + decode4(p.b_batch, bi) + decode4(p.b_n, ni);
-        float acc = 0.0f;
+        float* q = p.c + decode4(p.c_batch, bi) + decode4(p.c_m, mi) + decode4(p.c_n, ni);
+        float acc = p.beta == 0.0f ? 0.0f : p.beta * *q;
         uint32_t dig[4] = {0, 0, 0, 0};
         int64_t oa = 0, ob = 0;
         for (uint32_t kk = 0; kk < p.k; ++kk) {
-            acc = acc + a[oa] * b[ob];
+            acc = acc + (p.alpha * a[oa]) * b[ob];
 #pragma unroll
             for (int d = 3; d >= 0; --d) {
                 oa += p.a_k.stride[d];
@@ -119,10 +124,7 @@ __global__ __launch_bounds__(256) void general_f32(GeneralArgs p) {
                 dig[d] = 0;
             }
         }
-        float* q = p.c + decode4(p.c_batch, bi) + decode4(p.c_m, mi) + decode4(p.c_n, ni);
-        float v = p.alpha * acc;
-        if (p.beta != 0.0f) v = v + p.beta * *q;
-        *q = v;
+        *q = acc;
     }
 }
 

@@ -1,6 +1,7 @@
 // The fp32 MFMA GEMM kernel of the contraction path, parameterized by pipeline shape.
 //
-// gemm_f32_mfma<AM, BMD, BK, PIPE>: C = alpha * A.B + beta * C (or raw split-K partials) for
+// gemm_f32_mfma<AM, BMD, BK, PIPE>: C = beta * C + sum_k (alpha * a) * b (or raw split-K
+// partials of the sum) for
 // one stride per group. 128x128 output tile per 256-thread workgroup (4 waves in 2x2, each
 // wave 64x64 = 2x2 blocks of v_mfma_f32_32x32x2_f32 accumulating in fp32). K advances BK at a
 // time through two LDS stages: while the MFMAs consume stage s, the next K-slice is already in
@@ -106,18 +107,23 @@ __device__ inline void load_slice(floatx4 (&r)[Geo<BK>::LOADS], const float* __r
     }
 }
 
-template <int MODE, int BK>
+// Writes a loaded K-slice into its LDS stage. With SCALE (operand A) every element is first
+// multiplied by alpha, so each product the MFMAs form is (alpha*a)*b. alpha is finite here
+// (the planner sends non-finite alpha to the general kernel), so zero padding stays zero.
+template <int MODE, int BK, bool SCALE>
 __device__ inline void store_slice(float* __restrict__ st, const floatx4 (&r)[Geo<BK>::LOADS],
-                                   int tid) {
+                                   int tid, float alpha) {
 #pragma unroll
     for (int i = 0; i < Geo<BK>::LOADS; ++i) {
         const int idx = i * GEMM_THREADS + tid;
+        floatx4 v = r[i];
+        if constexpr (SCALE) v = v * alpha;
         if constexpr (MODE == LOAD_MN) {
             const int kr = idx / (BM / 4), row = (idx % (BM / 4)) * 4;
-            *reinterpret_cast<floatx4*>(st + kr * PMN + row) = r[i];
+            *reinterpret_cast<floatx4*>(st + kr * PMN + row) = v;
         } else {
             const int row = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
-            *reinterpret_cast<floatx4*>(st + row * Geo<BK>::PK + kq) = r[i];
+            *reinterpret_cast<floatx4*>(st + row * Geo<BK>::PK + kq) = v;
         }
     }
 }
@@ -201,8 +207,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
         }
     };
     load(0);
-    store_slice<AM, BK>(As, ra, tid);
-    store_slice<BMD, BK>(Bs, rb, tid);
+    store_slice<AM, BK, true>(As, ra, tid, p.alpha);
+    store_slice<BMD, BK, false>(Bs, rb, tid, 1.0f);
     __syncthreads();
 
     for (uint32_t kt = 0; kt < ktiles; ++kt) {
@@ -233,8 +239,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
             }
         }
         if (more) {
-            store_slice<AM, BK>(As + (s ^ 1) * A_ST, ra, tid);
-            store_slice<BMD, BK>(Bs + (s ^ 1) * B_ST, rb, tid);
+            store_slice<AM, BK, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
+            store_slice<BMD, BK, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);
         }
         __syncthreads();
     }
@@ -269,8 +275,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
                 if (inner || (row < p.m && col < p.n)) {
                     float* q = C + static_cast<int64_t>(row) * p.c_sm +
                                static_cast<int64_t>(col) * p.c_sn;
-                    float v = p.alpha * acc[i][j][r];
-                    if (p.beta != 0.0f) v = v + p.beta * *q;
+                    float v = acc[i][j][r];
+                    if (p.beta != 0.0f) v = p.beta * *q + v;
                     *q = v;
                 }
             }

@@ -117,7 +117,7 @@ struct ReduceArgs {
     float* c;
     int64_t c_sb, c_sm, c_sn;
     uint32_t m, n, batch, splits;
-    float alpha, beta;
+    float beta;
 };
 
 // Right-aligned mixed radix of up to 4 axes (slot 3 fastest); unused slots have extent 1.
@@ -201,6 +201,11 @@ struct lg_ctx : lg::Context {};
 
 namespace lg {
 void set_device(const lg_ctx* ctx);
+// Plans and enqueues the batched-matrix product C = alpha*A.B + beta*C on views whose ranges
+// the caller has already checked (the gemm form of the contraction planner; alias rules and
+// the scalar rules apply, views are not re-validated).
+void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
+                        float beta, const View& c);
 inline hipStream_t pick_stream(const lg_ctx* ctx, void* stream) {
     return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 }

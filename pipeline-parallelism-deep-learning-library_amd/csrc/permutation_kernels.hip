@@ -78,7 +78,7 @@ constexpr uint64_t COPY_GRID_CAP = 1u << 20;
 template <int W, bool CONJ, bool VEC, int TA, bool NT>
 void tile_t(hipStream_t s, const PermTileArgs& a) {
     const uint64_t g = perm_tile_workgroups(a.total_tiles);
-    hipLaunchKernelGGL((perm_tile<W, CONJ, VEC, TA, PERM_TILE_B, NT>),
+    hipLaunchKernelGGL((perm_tile<W, CONJ, VEC, TA, PERM_TILE_B, NT ? 3 : 0>),
                        dim3(static_cast<uint32_t>(g)), dim3(PERM_THREADS), 0, s, a);
 }
 

@@ -24,6 +24,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t SIGN = 0x80000000u;
 
 // 128-bit global accesses; NT marks them non-temporal (streamed past the caches).
+// Tile kernels take NTM: bit 0 makes the loads non-temporal, bit 1 the stores.
 template <bool NT>
 __device__ inline u32x4 load128(const uint32_t* p) {
     if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -35,8 +36,9 @@ __device__ inline void store128(uint32_t* p, u32x4 v) {
     else *reinterpret_cast<u32x4*>(p) = v;
 }
 
-template <int W, bool CONJ, bool VEC, int TA, int TB, bool NT = false>
+template <int W, bool CONJ, bool VEC, int TA, int TB, int NTM = 0>
 __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
+    constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;
     constexpr int VE = 4 / W;                       // elements per 128-bit word
     constexpr int PITCH = TA * W + 1;               // LDS row pitch in words (rows are b)
     constexpr int FILL_CHUNKS = TA * W / 4;         // 128-bit chunks per tile row (along a)
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             uint32_t* row = tile + bb * PITCH + cw;
             const int64_t e0 = sbase + static_cast<int64_t>(b) * p.src_sb + a;  // element index
             if (VEC && b < p.ext_b && a + VE <= p.ext_a) {
-                const u32x4 v = load128<NT>(src + e0 * W);
+                const u32x4 v = load128<NTL>(src + e0 * W);
                 row[0] = v[0];
                 row[1] = v[1];
                 row[2] = v[2];
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             }
             const int64_t e0 = dbase + static_cast<int64_t>(a) * p.dst_sa + b;
             if (VEC && a < p.ext_a && b + VE <= p.ext_b) {
-                store128<NT>(dst + e0 * W, v);
+                store128<NTS>(dst + e0 * W, v);
             } else {
 #pragma unroll
                 for (int e = 0; e < VE; ++e) {

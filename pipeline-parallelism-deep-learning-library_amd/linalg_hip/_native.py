@@ -16,6 +16,10 @@ LG_ALLOC_GRANULE = 16384
 
 LG_OK, LG_NO_DEVICE, LG_INVALID_ARGUMENT, LG_OVERLAP, LG_KERNEL = range(5)
 LG_ELEM_F32, LG_ELEM_U32, LG_ELEM_I32, LG_ELEM_C32 = range(4)
+# lg_core_error, in order: linalg_core::Error variants (crates/core/src/lib.rs:30-40).
+CORE_ERRORS = ["Ok", "Shape", "Dtype", "UnsupportedLayout", "UnsupportedDevice", "Alias",
+               "Transport", "Wire", "Schedule"]
+LG_DTYPE_F32, LG_DTYPE_F16, LG_DTYPE_BF16 = 1, 2, 3
 PLAN_KINDS = ["empty", "zero", "scale", "tiled", "split", "general"]
 LOAD_MODES = ["k", "mn", "strided"]
 PERMUTE_KINDS = ["empty", "copy", "tile"]
@@ -41,7 +45,14 @@ class lg_permute_plan(ctypes.Structure):
                 ("strides", u64 * 8), ("workgroups", u64)]
 
 
+class lg_tensor(ctypes.Structure):
+    _fields_ = [("base", vp), ("bytes", u64), ("dtype", u32), ("rank", u32), ("nstrides", u32),
+                ("reserved", u32), ("offset", u64), ("shape", u64 * LG_MAX_RANK),
+                ("strides", u64 * LG_MAX_RANK)]
+
+
 VP = ctypes.POINTER(lg_view)
+TP = ctypes.POINTER(lg_tensor)
 F = ctypes.c_float
 
 # name -> (restype, argtypes); every symbol the header declares.
@@ -72,6 +83,7 @@ SIGNATURES = {
     "lg_encode_gemm_f32": (i32, [vp, vp, F, VP, VP, F, VP]),
     "lg_gemm_f32": (i32, [vp, F, VP, VP, F, VP]),
     "lg_gemm_nowait_f32": (i32, [vp, F, VP, VP, F, VP]),
+    "lg_backend_gemm": (i32, [vp, vp, TP, TP, TP, F, F]),
     "lg_plan_contract_f32": (i32, [F, VP, cp, VP, cp, F, VP, cp,
                                    ctypes.POINTER(lg_contract_plan)]),
     "lg_plan_gemm_f32": (i32, [F, VP, VP, F, VP, ctypes.POINTER(lg_contract_plan)]),
