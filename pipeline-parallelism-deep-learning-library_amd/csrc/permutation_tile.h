@@ -7,9 +7,12 @@
 // b (destination unit stride). A TA x TB element tile is read with 128-bit loads running along
 // a, staged in LDS with an odd word pitch (TA*W + 1) so both the row-wise fill and the
 // column-wise drain spread over the banks, and written with 128-bit stores running along b.
-// Tiles are walked with a grid stride in the order (outer, tb, ta): the `a` tiles of one band
-// of source rows are consecutive, so concurrently running workgroups read whole source rows
-// (DRAM pages stay open) and write adjacent TB-element segments of the same destination rows.
+// Tiles are walked with a grid stride in the order (outer, ta, tb), tb fastest: concurrently
+// running workgroups write consecutive TB-element segments of the same TA destination rows, so
+// every destination row is written front to back, and read consecutive bands of source rows.
+// (On a 1 GiB transpose this order measured 2-3% faster than ta fastest on MI355X.)
+// A tile that lies wholly inside the view takes a branch-free path: all of its 128-bit loads
+// are issued before the first is waited on, and the drain reads LDS before it stores.
 // Ragged tile edges and misaligned views fall back to 32-bit word accesses.
 #pragma once
 
@@ -57,8 +60,8 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
     for (uint64_t t = blockIdx.x; t < p.total_tiles; t += gridDim.x) {
         uint64_t outer = t / per_outer;
         const uint64_t rem = t - outer * per_outer;
-        const uint32_t tb = static_cast<uint32_t>(rem / p.tiles_a);
-        const uint32_t ta = static_cast<uint32_t>(rem - static_cast<uint64_t>(tb) * p.tiles_a);
+        const uint32_t ta = static_cast<uint32_t>(rem / p.tiles_b);
+        const uint32_t tb = static_cast<uint32_t>(rem - static_cast<uint64_t>(ta) * p.tiles_b);
         int64_t sbase = static_cast<int64_t>(p.src_offset);
         int64_t dbase = static_cast<int64_t>(p.dst_offset);
         for (int d = static_cast<int>(p.outer_rank) - 1; d >= 0; --d) {
@@ -69,27 +72,53 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             outer = q;
         }
         const uint32_t a0 = ta * TA, b0 = tb * TB;
+        // Workgroup-uniform: the whole tile lies inside the view and 128-bit accesses are
+        // allowed. Then every load of the fill is issued before the first one is waited on,
+        // and the drain reads all its LDS words before its stores, with no per-chunk
+        // branches to serialize the memory pipeline.
+        const bool full = VEC && a0 + TA <= p.ext_a && b0 + TB <= p.ext_b;
 
         // Fill: rows of the tile are b, 128-bit chunks run along a.
+        if (full) {
+            u32x4 r[FILL_ITERS];
 #pragma unroll
-        for (int it = 0; it < FILL_ITERS; ++it) {
-            const int idx = it * PERM_THREADS + tid;
-            const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;  // word column
-            const uint32_t a = a0 + cw / W, b = b0 + bb;
-            uint32_t* row = tile + bb * PITCH + cw;
-            const int64_t e0 = sbase + static_cast<int64_t>(b) * p.src_sb + a;  // element index
-            if (VEC && b < p.ext_b && a + VE <= p.ext_a) {
-                const u32x4 v = load128<NTL>(src + e0 * W);
-                row[0] = v[0];
-                row[1] = v[1];
-                row[2] = v[2];
-                row[3] = v[3];
-            } else {
+            for (int it = 0; it < FILL_ITERS; ++it) {
+                const int idx = it * PERM_THREADS + tid;
+                const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
+                const int64_t e0 = sbase + static_cast<int64_t>(b0 + bb) * p.src_sb + a0 + cw / W;
+                r[it] = load128<NTL>(src + e0 * W);
+            }
 #pragma unroll
-                for (int e = 0; e < VE; ++e) {
-                    if (b < p.ext_b && a + e < p.ext_a) {
+            for (int it = 0; it < FILL_ITERS; ++it) {
+                const int idx = it * PERM_THREADS + tid;
+                const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
+                uint32_t* row = tile + bb * PITCH + cw;
+                row[0] = r[it][0];
+                row[1] = r[it][1];
+                row[2] = r[it][2];
+                row[3] = r[it][3];
+            }
+        } else {
 #pragma unroll
-                        for (int w = 0; w < W; ++w) row[e * W + w] = src[(e0 + e) * W + w];
+            for (int it = 0; it < FILL_ITERS; ++it) {
+                const int idx = it * PERM_THREADS + tid;
+                const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;  // word column
+                const uint32_t a = a0 + cw / W, b = b0 + bb;
+                uint32_t* row = tile + bb * PITCH + cw;
+                const int64_t e0 = sbase + static_cast<int64_t>(b) * p.src_sb + a;  // element
+                if (VEC && b < p.ext_b && a + VE <= p.ext_a) {
+                    const u32x4 v = load128<NTL>(src + e0 * W);
+                    row[0] = v[0];
+                    row[1] = v[1];
+                    row[2] = v[2];
+                    row[3] = v[3];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VE; ++e) {
+                        if (b < p.ext_b && a + e < p.ext_a) {
+#pragma unroll
+                            for (int w = 0; w < W; ++w) row[e * W + w] = src[(e0 + e) * W + w];
+                        }
                     }
                 }
             }
@@ -97,12 +126,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
         __syncthreads();
 
         // Drain: 128-bit chunks run along b, one destination row per a.
-#pragma unroll
-        for (int it = 0; it < DRAIN_ITERS; ++it) {
-            const int idx = it * PERM_THREADS + tid;
-            const int aa = idx / DRAIN_CHUNKS, cw = (idx % DRAIN_CHUNKS) * 4;
-            const int bl = cw / W;  // first b (local) of this chunk
-            const uint32_t a = a0 + aa, b = b0 + bl;
+        auto gather = [&](int aa, int bl) {
             u32x4 v;
 #pragma unroll
             for (int e = 0; e < VE; ++e) {
@@ -113,143 +137,45 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
                     v[e * W + w] = word;
                 }
             }
-            const int64_t e0 = dbase + static_cast<int64_t>(a) * p.dst_sa + b;
-            if (VEC && a < p.ext_a && b + VE <= p.ext_b) {
-                store128<NTS>(dst + e0 * W, v);
-            } else {
+            return v;
+        };
+        if (full) {
+            u32x4 v[DRAIN_ITERS];
 #pragma unroll
-                for (int e = 0; e < VE; ++e) {
-                    if (a < p.ext_a && b + e < p.ext_b) {
+            for (int it = 0; it < DRAIN_ITERS; ++it) {
+                const int idx = it * PERM_THREADS + tid;
+                v[it] = gather(idx / DRAIN_CHUNKS, (idx % DRAIN_CHUNKS) * 4 / W);
+            }
 #pragma unroll
-                        for (int w = 0; w < W; ++w) dst[(e0 + e) * W + w] = v[e * W + w];
+            for (int it = 0; it < DRAIN_ITERS; ++it) {
+                const int idx = it * PERM_THREADS + tid;
+                const int aa = idx / DRAIN_CHUNKS, bl = (idx % DRAIN_CHUNKS) * 4 / W;
+                const int64_t e0 = dbase + static_cast<int64_t>(a0 + aa) * p.dst_sa + b0 + bl;
+                store128<NTS>(dst + e0 * W, v[it]);
+            }
+        } else {
+#pragma unroll
+            for (int it = 0; it < DRAIN_ITERS; ++it) {
+                const int idx = it * PERM_THREADS + tid;
+                const int aa = idx / DRAIN_CHUNKS, cw = (idx % DRAIN_CHUNKS) * 4;
+                const int bl = cw / W;  // first b (local) of this chunk
+                const uint32_t a = a0 + aa, b = b0 + bl;
+                const u32x4 v = gather(aa, bl);
+                const int64_t e0 = dbase + static_cast<int64_t>(a) * p.dst_sa + b;
+                if (VEC && a < p.ext_a && b + VE <= p.ext_b) {
+                    store128<NTS>(dst + e0 * W, v);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VE; ++e) {
+                        if (a < p.ext_a && b + e < p.ext_b) {
+#pragma unroll
+                            for (int w = 0; w < W; ++w) dst[(e0 + e) * W + w] = v[e * W + w];
+                        }
                     }
                 }
             }
         }
         __syncthreads();
-    }
-}
-
-
-// Software-pipelined variant for views that allow 128-bit accesses: each workgroup walks
-// several tiles and, after staging tile t in LDS, issues the HBM reads of its next tile before
-// draining tile t, so the read and write streams of one workgroup overlap.
-template <int W, bool CONJ, int TA, int TB, bool NT>
-__global__ __launch_bounds__(PERM_THREADS) void perm_tile_pipe(PermTileArgs p) {
-    constexpr int VE = 4 / W;
-    constexpr int PITCH = TA * W + 1;
-    constexpr int FILL_CHUNKS = TA * W / 4;
-    constexpr int DRAIN_CHUNKS = TB * W / 4;
-    constexpr int FILL_ITERS = TB * FILL_CHUNKS / PERM_THREADS;
-    constexpr int DRAIN_ITERS = TA * DRAIN_CHUNKS / PERM_THREADS;
-    static_assert(FILL_ITERS * PERM_THREADS == TB * FILL_CHUNKS, "fill must split evenly");
-    static_assert(DRAIN_ITERS * PERM_THREADS == TA * DRAIN_CHUNKS, "drain must split evenly");
-    __shared__ uint32_t tile[TB * PITCH];
-
-    const uint32_t* src = static_cast<const uint32_t*>(p.src);
-    uint32_t* dst = static_cast<uint32_t*>(p.dst);
-    const int tid = threadIdx.x;
-    const uint64_t per_outer = static_cast<uint64_t>(p.tiles_a) * p.tiles_b;
-
-    struct Pos {
-        int64_t sbase, dbase;
-        uint32_t a0, b0;
-    };
-    auto locate = [&](uint64_t t) {
-        Pos q;
-        uint64_t outer = t / per_outer;
-        const uint64_t rem = t - outer * per_outer;
-        const uint32_t tb = static_cast<uint32_t>(rem / p.tiles_a);
-        const uint32_t ta = static_cast<uint32_t>(rem - static_cast<uint64_t>(tb) * p.tiles_a);
-        q.sbase = static_cast<int64_t>(p.src_offset);
-        q.dbase = static_cast<int64_t>(p.dst_offset);
-        for (int d = static_cast<int>(p.outer_rank) - 1; d >= 0; --d) {
-            const uint64_t qq = outer / p.outer_shape[d];
-            const int64_t c = static_cast<int64_t>(outer - qq * p.outer_shape[d]);
-            q.sbase += c * p.outer_src[d];
-            q.dbase += c * p.outer_dst[d];
-            outer = qq;
-        }
-        q.a0 = ta * TA;
-        q.b0 = tb * TB;
-        return q;
-    };
-    u32x4 r[FILL_ITERS];
-    auto fetch = [&](const Pos& q) {
-#pragma unroll
-        for (int it = 0; it < FILL_ITERS; ++it) {
-            const int idx = it * PERM_THREADS + tid;
-            const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
-            const uint32_t a = q.a0 + cw / W, b = q.b0 + bb;
-            const int64_t e0 = q.sbase + static_cast<int64_t>(b) * p.src_sb + a;
-            if (b < p.ext_b && a + VE <= p.ext_a) {
-                r[it] = load128<NT>(src + e0 * W);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VE; ++e)
-#pragma unroll
-                    for (int w = 0; w < W; ++w)
-                        r[it][e * W + w] = (b < p.ext_b && a + e < p.ext_a) ? src[(e0 + e) * W + w] : 0u;
-            }
-        }
-    };
-
-    uint64_t t = blockIdx.x;
-    if (t >= p.total_tiles) return;
-    Pos cur = locate(t);
-    fetch(cur);
-    for (;;) {
-#pragma unroll
-        for (int it = 0; it < FILL_ITERS; ++it) {
-            const int idx = it * PERM_THREADS + tid;
-            const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
-            uint32_t* row = tile + bb * PITCH + cw;
-            row[0] = r[it][0];
-            row[1] = r[it][1];
-            row[2] = r[it][2];
-            row[3] = r[it][3];
-        }
-        __syncthreads();
-        const uint64_t tn = t + gridDim.x;
-        const bool more = tn < p.total_tiles;
-        Pos next = cur;
-        if (more) {
-            next = locate(tn);
-            fetch(next);
-        }
-#pragma unroll
-        for (int it = 0; it < DRAIN_ITERS; ++it) {
-            const int idx = it * PERM_THREADS + tid;
-            const int aa = idx / DRAIN_CHUNKS, cw = (idx % DRAIN_CHUNKS) * 4;
-            const int bl = cw / W;
-            const uint32_t a = cur.a0 + aa, b = cur.b0 + bl;
-            u32x4 v;
-#pragma unroll
-            for (int e = 0; e < VE; ++e) {
-#pragma unroll
-                for (int w = 0; w < W; ++w) {
-                    uint32_t word = tile[(bl + e) * PITCH + aa * W + w];
-                    if (CONJ && w == 1) word ^= SIGN;
-                    v[e * W + w] = word;
-                }
-            }
-            const int64_t e0 = cur.dbase + static_cast<int64_t>(a) * p.dst_sa + b;
-            if (a < p.ext_a && b + VE <= p.ext_b) {
-                store128<NT>(dst + e0 * W, v);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VE; ++e) {
-                    if (a < p.ext_a && b + e < p.ext_b) {
-#pragma unroll
-                        for (int w = 0; w < W; ++w) dst[(e0 + e) * W + w] = v[e * W + w];
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        if (!more) break;
-        t = tn;
-        cur = next;
     }
 }
 
