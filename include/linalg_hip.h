@@ -234,6 +234,56 @@ typedef struct lg_tensor {
 lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_tensor* a, const lg_tensor* b,
                               const lg_tensor* c, float alpha, float beta);
 
+/* The Backend trait's activation and training ops (crates/core/src/lib.rs:165-255), each with
+ * CpuBackend's check order and error codes (crates/cpu/src/lib.rs:297-533) and one kernel
+ * launch. Every check runs before `ctx` is used, and on any error nothing is launched or
+ * written. A dtype tag outside lg_dtype is LG_CORE_WIRE. Operands are row-major contiguous at
+ * offset 0 (else LG_CORE_UNSUPPORTED_LAYOUT) whose storage holds all their bytes (else
+ * LG_CORE_SHAPE). Each formula is evaluated as written, one rounding per operation; empty
+ * operands launch nothing. All but mse_grad enqueue on `stream` (NULL = context stream) and
+ * return before the device finishes. */
+
+/* gelu (crates/cpu/src/lib.rs:297-307): y = 0.5*x*(1 + erf(x/sqrt 2)), erf by Abramowitz &
+ * Stegun 7.1.26 in f32 as the reference evaluates it. Checks: Dtype (all f32), Shape (equal
+ * shapes), layout, storage. y may be x. */
+lg_core_error lg_backend_gelu(lg_ctx* ctx, void* stream, const lg_tensor* x, const lg_tensor* y);
+
+/* gelu_backward (crates/cpu/src/lib.rs:309-326): dx = dy * (Phi(pre) + pre*phi(pre)).
+ * Checks as gelu over (pre, dy, dx). */
+lg_core_error lg_backend_gelu_backward(lg_ctx* ctx, void* stream, const lg_tensor* pre,
+                                       const lg_tensor* dy, const lg_tensor* dx);
+
+/* add_bias (crates/cpu/src/lib.rs:372-401): y[i][j] = x[i][j] + b[j]; x, y [B, N], b [N].
+ * Checks: Shape, Dtype, Alias (b distinct from x and y; y may be x), layout, storage. */
+lg_core_error lg_backend_add_bias(lg_ctx* ctx, void* stream, const lg_tensor* x,
+                                  const lg_tensor* b, const lg_tensor* y);
+
+/* bias_grad (crates/cpu/src/lib.rs:403-435): db[j] = db[j] + (dpre[0][j] + dpre[1][j] + ...),
+ * rows summed in order as the reference does, so the result is the reference's bits.
+ * Checks: Shape (dpre [B, N], db [N]), Dtype, Alias, layout, storage; B, N < 2^32. */
+lg_core_error lg_backend_bias_grad(lg_ctx* ctx, void* stream, const lg_tensor* dpre,
+                                   const lg_tensor* db);
+
+/* mse_grad (crates/cpu/src/lib.rs:437-472): d = y - target, dy = (2*d)/n, *loss = (sum of
+ * d*d)/n with n rounded to f32. The loss sums in a fixed order that depends only on n (the
+ * contract leaves the order to the backend). Checks: Shape (equal shapes, n > 0), Dtype,
+ * Alias (dy distinct from target; dy may be y, y may share target's storage), layout,
+ * storage. Waits for every earlier call and this one before returning; *loss is unchanged on
+ * error. */
+lg_core_error lg_backend_mse_grad(lg_ctx* ctx, void* stream, const lg_tensor* y,
+                                  const lg_tensor* target, const lg_tensor* dy, float* loss);
+
+/* sgd_step (crates/cpu/src/lib.rs:474-501): w = w - (lr*dw), then dw = +0. Checks: Shape,
+ * Dtype, Alias (distinct storage), layout, storage. */
+lg_core_error lg_backend_sgd_step(lg_ctx* ctx, void* stream, const lg_tensor* w,
+                                  const lg_tensor* dw, float lr);
+
+/* convert (crates/cpu/src/lib.rs:503-533,725-732): F32 -> BF16 nearest, ties to even (NaN
+ * stays a quiet NaN of the same sign, overflow to infinity, subnormals kept); BF16 -> F32
+ * exact. Checks: Shape, Dtype ((F32, BF16) or (BF16, F32)), Alias, layout, storage. */
+lg_core_error lg_backend_convert(lg_ctx* ctx, void* stream, const lg_tensor* x,
+                                 const lg_tensor* y);
+
 /* ---------------------------------------------------------------------------------------
  * Plan inspection (host only; no context, no device work). These run the exact
  * validation and planning of the entry points above and report the plan instead of

@@ -12,6 +12,9 @@ Functions (C implementations in oracle.c, each citing the reference code it rest
   contract_f64    tests/contraction_test.rs:200-268 (f64 accumulation, error magnitude)
   gate            tests/contraction_test.rs:280-313 accuracy gate
   north_star_tol  max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|
+  gelu, gelu_backward, add_bias, bias_grad, mse_grad, sgd_step, f32_to_bf16, bf16_to_f32
+                  the CpuBackend activation and training ops (crates/cpu/src/lib.rs:297-533,
+                  722-729, 809-842), sequential, one rounding per operation
 """
 from __future__ import annotations
 
@@ -58,6 +61,20 @@ def lib():
                                           i64p, i64p, i64p, ctypes.c_uint32, u64p, i64p, i64p,
                                           f32p, u64, f32p, u64, f32p, u64, dp, dp, u64p]
         L.oracle_contract_f64.restype = None
+        vp = ctypes.c_void_p
+        L.oracle_erf_constants.argtypes = [vp]
+        L.oracle_erf_constants.restype = None
+        for name, args in [("oracle_gelu_f32", [vp, vp, u64]),
+                           ("oracle_gelu_backward_f32", [vp, vp, vp, u64]),
+                           ("oracle_add_bias_f32", [vp, vp, vp, u64, u64]),
+                           ("oracle_bias_grad_f32", [vp, vp, u64, u64]),
+                           ("oracle_sgd_step_f32", [vp, vp, ctypes.c_float, u64]),
+                           ("oracle_f32_to_bf16", [vp, vp, u64]),
+                           ("oracle_bf16_to_f32", [vp, vp, u64])]:
+            getattr(L, name).argtypes = args
+            getattr(L, name).restype = None
+        L.oracle_mse_grad_f32.argtypes = [vp, vp, vp, u64]
+        L.oracle_mse_grad_f32.restype = ctypes.c_float
         _lib = L
     return _lib
 
@@ -187,3 +204,74 @@ def north_star_tol(k: int, a: np.ndarray, b: np.ndarray) -> float:
     ma = float(np.max(np.abs(a))) if a.size else 0.0
     mb = float(np.max(np.abs(b))) if b.size else 0.0
     return 1e-5 * max(k, 1) ** 0.5 * ma * mb
+
+
+# ---- Backend activation and training ops --------------------------------------------------
+def _f32(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a
+
+
+def erf_constants() -> list:
+    out = np.zeros(6, dtype=np.uint32)
+    lib().oracle_erf_constants(out.ctypes.data)
+    return [int(v) for v in out]
+
+
+def gelu(x) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().oracle_gelu_f32(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def gelu_backward(pre, dy) -> np.ndarray:
+    pre, dy = _f32(pre), _f32(dy)
+    dx = np.empty_like(pre)
+    lib().oracle_gelu_backward_f32(pre.ctypes.data, dy.ctypes.data, dx.ctypes.data, pre.size)
+    return dx
+
+
+def add_bias(x, b) -> np.ndarray:
+    x, b = _f32(x), _f32(b)
+    y = np.empty_like(x)
+    rows, cols = x.shape
+    lib().oracle_add_bias_f32(x.ctypes.data, b.ctypes.data, y.ctypes.data, rows, cols)
+    return y
+
+
+def bias_grad(dpre, db) -> np.ndarray:
+    dpre = _f32(dpre)
+    out = _f32(db).copy()
+    rows, cols = dpre.shape
+    lib().oracle_bias_grad_f32(dpre.ctypes.data, out.ctypes.data, rows, cols)
+    return out
+
+
+def mse_grad(y, t):
+    """(dy, loss) of CpuBackend::mse_grad."""
+    y, t = _f32(y), _f32(t)
+    dy = np.empty_like(y)
+    loss = lib().oracle_mse_grad_f32(y.ctypes.data, t.ctypes.data, dy.ctypes.data, y.size)
+    return dy, np.float32(loss)
+
+
+def sgd_step(w, dw, lr):
+    """(w', dw') of CpuBackend::sgd_step."""
+    w, dw = _f32(w).copy(), _f32(dw).copy()
+    lib().oracle_sgd_step_f32(w.ctypes.data, dw.ctypes.data, float(lr), w.size)
+    return w, dw
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).view(np.uint32))
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_bf16(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.uint32)
+    lib().oracle_bf16_to_f32(h.ctypes.data, y.ctypes.data, h.size)
+    return y.view(np.float32)

@@ -16,7 +16,9 @@
  * (identity / permutation / integer matrices), and each other bit for bit; the gather
  * against numpy.transpose on raw words and the complex word table of
  * tests/permutation_test.rs:464-492; the f64 reference against numpy float64 einsum and
- * exact integer cases.
+ * exact integer cases; the training ops against the reference's own known answers and f64
+ * bounds (crates/cpu/src/training.rs, crates/cpu/src/invariants.rs:446-500), the constants'
+ * asserted bit patterns, and the exhaustive bf16 table (tests/test_training_oracle.py).
  */
 #include <math.h>
 #include <pthread.h>
@@ -247,4 +249,116 @@ void oracle_contract_f64(float alpha_f, float beta_f, uint32_t n_free, const uin
             fi[d] = 0;
         }
     }
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Backend activation and training ops (crates/cpu/src/lib.rs:297-533,722-729,809-842).
+ * Arrays are dense row-major; every expression is the reference's, in its order, one
+ * rounding per operation. expf is the C library's, which is what Rust's f32::exp calls on
+ * Linux.
+ * ---------------------------------------------------------------------------------------- */
+
+/* The f32 spellings of A&S 7.1.26's coefficients and 1/sqrt(2 pi) the reference asserts
+ * (crates/cpu/src/lib.rs:845-857): 0.2548296, 0.28449672, 1.4214138, 1.4531521, 1.0614054,
+ * 0.3989423. */
+static const float ERF_A1 = 0.2548296f;
+static const float ERF_A2 = 0.28449672f;
+static const float ERF_A3 = 1.4214138f;
+static const float ERF_A4 = 1.4531521f;
+static const float ERF_A5 = 1.0614054f;
+static const float INV_SQRT_2PI = 0.3989423f;
+static const float FRAC_1_SQRT_2_F = 0.70710677f; /* std::f32::consts::FRAC_1_SQRT_2 */
+
+/* Bit patterns of the six constants above, for the pinning test. */
+void oracle_erf_constants(uint32_t out[6]) {
+    const float v[6] = {ERF_A1, ERF_A2, ERF_A3, ERF_A4, ERF_A5, INV_SQRT_2PI};
+    memcpy(out, v, sizeof v);
+}
+
+/* erf_f32 (crates/cpu/src/lib.rs:811-817). */
+static float erf_as(float x) {
+    const float sign = signbit(x) ? -1.0f : 1.0f;
+    const float a = fabsf(x);
+    const float t = 1.0f / (1.0f + 0.3275911f * a);
+    const float poly = (((((ERF_A5 * t - ERF_A4) * t) + ERF_A3) * t - ERF_A2) * t + ERF_A1) * t;
+    return sign * (1.0f - poly * expf(-a * a));
+}
+
+/* gelu_f32 / gelu_prime_f32 (crates/cpu/src/lib.rs:820-829). */
+static float gelu_one(float x) {
+    const float inner = x * FRAC_1_SQRT_2_F;
+    return 0.5f * x * (1.0f + erf_as(inner));
+}
+
+static float gelu_prime_one(float x) {
+    const float phi = 0.5f * (1.0f + erf_as(x * FRAC_1_SQRT_2_F));
+    const float pdf = expf(-0.5f * x * x) * INV_SQRT_2PI;
+    return phi + x * pdf;
+}
+
+/* CpuBackend::gelu (crates/cpu/src/lib.rs:297-307). */
+void oracle_gelu_f32(const float* x, float* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) y[i] = gelu_one(x[i]);
+}
+
+/* CpuBackend::gelu_backward (crates/cpu/src/lib.rs:309-326): dx = dy * GELU'(pre). */
+void oracle_gelu_backward_f32(const float* pre, const float* dy, float* dx, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) dx[i] = dy[i] * gelu_prime_one(pre[i]);
+}
+
+/* CpuBackend::add_bias (crates/cpu/src/lib.rs:372-401). y may be x. */
+void oracle_add_bias_f32(const float* x, const float* b, float* y, uint64_t rows, uint64_t cols) {
+    for (uint64_t r = 0; r < rows; ++r)
+        for (uint64_t c = 0; c < cols; ++c) y[r * cols + c] = x[r * cols + c] + b[c];
+}
+
+/* CpuBackend::bias_grad (crates/cpu/src/lib.rs:403-435): per column, rows summed in order
+ * from +0, then db[j] + s. */
+void oracle_bias_grad_f32(const float* dpre, float* db, uint64_t rows, uint64_t cols) {
+    if (rows == 0) return;
+    for (uint64_t c = 0; c < cols; ++c) {
+        float s = 0.0f;
+        for (uint64_t r = 0; r < rows; ++r) s += dpre[r * cols + c];
+        db[c] = db[c] + s;
+    }
+}
+
+/* CpuBackend::mse_grad (crates/cpu/src/lib.rs:437-472): one pass in index order. dy may be
+ * y. Returns the loss. */
+float oracle_mse_grad_f32(const float* y, const float* t, float* dy, uint64_t n) {
+    const float nf = (float)n;
+    float sum = 0.0f;
+    for (uint64_t i = 0; i < n; ++i) {
+        const float d = y[i] - t[i];
+        sum += d * d;
+        dy[i] = (2.0f * d) / nf;
+    }
+    return sum / nf;
+}
+
+/* CpuBackend::sgd_step (crates/cpu/src/lib.rs:474-501). */
+void oracle_sgd_step_f32(float* w, float* dw, float lr, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const float step = lr * dw[i];
+        w[i] = w[i] - step;
+        dw[i] = 0.0f;
+    }
+}
+
+/* f32_bits_to_bf16 (crates/cpu/src/lib.rs:725-732) and the bf16 -> f32 widening of
+ * CpuBackend::convert (crates/cpu/src/lib.rs:519-527). */
+void oracle_f32_to_bf16(const uint32_t* x, uint16_t* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t bits = x[i];
+        if ((bits & 0x7fffffffu) > 0x7f800000u) {
+            y[i] = (uint16_t)((bits >> 16) | 0x0040u);
+        } else {
+            const uint32_t lsb = (bits >> 16) & 1u;
+            y[i] = (uint16_t)((bits + 0x7fffu + lsb) >> 16);
+        }
+    }
+}
+
+void oracle_bf16_to_f32(const uint16_t* x, uint32_t* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) y[i] = (uint32_t)x[i] << 16;
 }

@@ -28,6 +28,7 @@ SOURCES = [
     "permutation.cpp",
     "contraction_kernels.hip",
     "permutation_kernels.hip",
+    "training_kernels.hip",
 ]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

@@ -85,10 +85,264 @@ View to_view(const lg_tensor* t) {
     return v;
 }
 
+// ---- training-op checks (crates/cpu/src/lib.rs:297-533,595-604,731-807) ----------------
+
+// Every tensor handed in: non-null, a decodable dtype tag, rank and stride count that fit.
+void decode(std::initializer_list<const lg_tensor*> ts) {
+    for (const lg_tensor* t : ts) {
+        if (t == nullptr) core_fail(LG_CORE_SHAPE, "null tensor");
+        if (t->rank > LG_MAX_RANK || t->nstrides > LG_MAX_RANK) {
+            core_fail(LG_CORE_SHAPE, "rank above LG_MAX_RANK");
+        }
+    }
+    for (const lg_tensor* t : ts) dtype_size(t->dtype);
+}
+
+bool same_shape(const lg_tensor* a, const lg_tensor* b) {
+    if (a->rank != b->rank) return false;
+    for (uint32_t d = 0; d < a->rank; ++d) {
+        if (a->shape[d] != b->shape[d]) return false;
+    }
+    return true;
+}
+
+// numel with overflow as Shape (numel, crates/cpu/src/lib.rs:595-601).
+uint64_t numel(const lg_tensor* t) {
+    uint64_t n = 1;
+    for (uint32_t d = 0; d < t->rank; ++d) {
+        if (t->shape[d] != 0 && n > UINT64_MAX / t->shape[d]) core_fail(LG_CORE_SHAPE, "element count overflows");
+        n *= t->shape[d];
+    }
+    return n;
+}
+
+uint64_t nbytes(const lg_tensor* t) {
+    const uint64_t n = numel(t), size = dtype_size(t->dtype);
+    if (n > UINT64_MAX / size) core_fail(LG_CORE_SHAPE, "byte count overflows");
+    return n * size;
+}
+
+// packed_layout (crates/cpu/src/lib.rs:731-744): offset 0, row-major strides.
+bool packed_layout(const lg_tensor* t) {
+    if (t->offset != 0 || t->nstrides != t->rank) return false;
+    uint64_t stride = 1;
+    for (uint32_t d = t->rank; d-- > 0;) {
+        if (t->strides[d] != stride) return false;
+        stride *= t->shape[d];  // wraps like the reference's wrapping_mul
+    }
+    return true;
+}
+
+void all_f32(std::initializer_list<const lg_tensor*> ts) {
+    for (const lg_tensor* t : ts) {
+        if (t->dtype != LG_DTYPE_F32) core_fail(LG_CORE_DTYPE, "operand is not f32");
+    }
+}
+
+// packed (crates/cpu/src/lib.rs:769-781): layout first, then each storage holds its bytes.
+void packed(std::initializer_list<const lg_tensor*> ts) {
+    for (const lg_tensor* t : ts) {
+        if (!packed_layout(t)) core_fail(LG_CORE_UNSUPPORTED_LAYOUT, "operand is not row-major contiguous at offset 0");
+    }
+    for (const lg_tensor* t : ts) {
+        if (nbytes(t) > t->bytes) core_fail(LG_CORE_SHAPE, "operand reaches past its storage");
+    }
+}
+
+// prepare_f32_row_major (crates/cpu/src/lib.rs:783-807): Dtype, Shape, layout, storage.
+uint64_t prepare_f32_row_major(std::initializer_list<const lg_tensor*> ts) {
+    all_f32(ts);
+    const lg_tensor* first = *ts.begin();
+    for (const lg_tensor* t : ts) {
+        if (!same_shape(t, first)) core_fail(LG_CORE_SHAPE, "shapes differ");
+    }
+    for (const lg_tensor* t : ts) {
+        if (t->offset != 0 || t->nstrides != t->rank) {
+            core_fail(LG_CORE_UNSUPPORTED_LAYOUT, "operand is not row-major contiguous at offset 0");
+        }
+        uint64_t stride = 1;
+        for (uint32_t d = t->rank; d-- > 0;) {
+            if (t->strides[d] != stride) {
+                core_fail(LG_CORE_UNSUPPORTED_LAYOUT, "operand is not row-major contiguous at offset 0");
+            }
+            stride *= t->shape[d];
+        }
+    }
+    const uint64_t count = numel(first);
+    if (count > UINT64_MAX / 4) core_fail(LG_CORE_SHAPE, "byte count overflows");
+    for (const lg_tensor* t : ts) {
+        if (t->bytes < count * 4) core_fail(LG_CORE_SHAPE, "operand reaches past its storage");
+    }
+    return count;
+}
+
+// Runs `body` (checks, then launches) with the entry points' error mapping: check failures
+// return their code; device failures return UnsupportedDevice with the HIP message.
+template <typename F>
+lg_core_error run_op(F&& body) {
+    try {
+        body();
+        clear_last_error();
+        return LG_CORE_OK;
+    } catch (const TensorErr& e) {
+        set_last_error(e.message);
+        return e.code;
+    } catch (const Failure& f) {
+        set_last_error(f.message);
+        return LG_CORE_UNSUPPORTED_DEVICE;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return LG_CORE_UNSUPPORTED_DEVICE;
+    }
+}
+
+hipStream_t device_stream(lg_ctx* ctx, void* stream) {
+    if (ctx == nullptr) core_fail(LG_CORE_UNSUPPORTED_DEVICE, "null context");
+    set_device(ctx);
+    return pick_stream(ctx, stream);
+}
+
+template <typename T>
+T* dev(const lg_tensor* t) {
+    return static_cast<T*>(t->base);
+}
+
 }  // namespace
 }  // namespace lg
 
 using namespace lg;
+
+extern "C" {
+
+lg_core_error lg_backend_gelu(lg_ctx* ctx, void* stream, const lg_tensor* x, const lg_tensor* y) {
+    return run_op([&] {
+        decode({x, y});
+        const uint64_t n = prepare_f32_row_major({x, y});
+        hipStream_t s = device_stream(ctx, stream);
+        if (n > 0) launch_gelu(ctx, s, dev<const float>(x), dev<float>(y), n);
+    });
+}
+
+lg_core_error lg_backend_gelu_backward(lg_ctx* ctx, void* stream, const lg_tensor* pre,
+                                       const lg_tensor* dy, const lg_tensor* dx) {
+    return run_op([&] {
+        decode({pre, dy, dx});
+        const uint64_t n = prepare_f32_row_major({pre, dy, dx});
+        hipStream_t s = device_stream(ctx, stream);
+        if (n > 0) launch_gelu_backward(ctx, s, dev<const float>(pre), dev<const float>(dy), dev<float>(dx), n);
+    });
+}
+
+lg_core_error lg_backend_add_bias(lg_ctx* ctx, void* stream, const lg_tensor* x,
+                                  const lg_tensor* b, const lg_tensor* y) {
+    return run_op([&] {
+        decode({x, b, y});
+        // bias_shapes (crates/cpu/src/lib.rs:746-757).
+        if (x->rank != 2 || !same_shape(y, x) || b->rank != 1 || b->shape[0] != x->shape[1]) {
+            core_fail(LG_CORE_SHAPE, "add_bias needs x [B, N], b [N], y [B, N]");
+        }
+        all_f32({x, b, y});
+        if (b->base == x->base || b->base == y->base) core_fail(LG_CORE_ALIAS, "b shares storage with x or y");
+        packed({x, b, y});
+        hipStream_t s = device_stream(ctx, stream);
+        const uint64_t rows = x->shape[0], cols = x->shape[1];
+        if (rows > 0 && cols > 0) launch_add_bias(ctx, s, dev<const float>(x), dev<const float>(b), dev<float>(y), rows, cols);
+    });
+}
+
+lg_core_error lg_backend_bias_grad(lg_ctx* ctx, void* stream, const lg_tensor* dpre,
+                                   const lg_tensor* db) {
+    return run_op([&] {
+        decode({dpre, db});
+        if (dpre->rank != 2 || db->rank != 1 || db->shape[0] != dpre->shape[1]) {
+            core_fail(LG_CORE_SHAPE, "bias_grad needs dpre [B, N] and db [N]");
+        }
+        all_f32({dpre, db});
+        if (dpre->base == db->base) core_fail(LG_CORE_ALIAS, "db shares storage with dpre");
+        packed({dpre, db});
+        const uint64_t rows = dpre->shape[0], cols = dpre->shape[1];
+        if (rows > 0xffffffffull || cols > 0xffffffffull) {
+            core_fail(LG_CORE_SHAPE, "bias_grad extents must fit 32 bits");
+        }
+        hipStream_t s = device_stream(ctx, stream);
+        if (rows > 0 && cols > 0) {
+            launch_bias_grad(ctx, s, dev<const float>(dpre), dev<float>(db), static_cast<uint32_t>(rows),
+                             static_cast<uint32_t>(cols));
+        }
+    });
+}
+
+lg_core_error lg_backend_mse_grad(lg_ctx* ctx, void* stream, const lg_tensor* y,
+                                  const lg_tensor* target, const lg_tensor* dy, float* loss) {
+    return run_op([&] {
+        decode({y, target, dy});
+        if (!same_shape(target, y) || !same_shape(dy, y)) core_fail(LG_CORE_SHAPE, "shapes differ");
+        const uint64_t n = numel(y);
+        if (n == 0) core_fail(LG_CORE_SHAPE, "mse_grad of zero elements");
+        all_f32({y, target, dy});
+        if (dy->base == target->base) core_fail(LG_CORE_ALIAS, "dy shares storage with target");
+        packed({y, target, dy});
+        if (loss == nullptr) core_fail(LG_CORE_SHAPE, "null loss pointer");
+        hipStream_t s = device_stream(ctx, stream);
+        uint64_t chunk = 0;
+        const uint64_t groups = mse_groups(n, &chunk);
+        // Scratch: partial[groups], then the counter, then the loss; stream-ordered.
+        const size_t bytes = (groups + 2) * sizeof(float);
+        void* scratch = nullptr;
+        check_hip(hipMallocAsync(&scratch, bytes, s), "hipMallocAsync");
+        float* partial = static_cast<float*>(scratch);
+        uint32_t* counter = reinterpret_cast<uint32_t*>(partial + groups);
+        float* dloss = partial + groups + 1;
+        float host = 0.0f;
+        hipError_t e = hipMemsetAsync(counter, 0, sizeof(uint32_t), s);
+        if (e == hipSuccess) {
+            try {
+                launch_mse_grad(ctx, s, dev<const float>(y), dev<const float>(target), dev<float>(dy), n,
+                                partial, counter, dloss);
+            } catch (...) {
+                (void)hipFreeAsync(scratch, s);
+                throw;
+            }
+            e = hipMemcpyAsync(&host, dloss, sizeof(float), hipMemcpyDeviceToHost, s);
+        }
+        const hipError_t f = hipFreeAsync(scratch, s);
+        check_hip(e, "mse_grad");
+        check_hip(f, "hipFreeAsync");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        *loss = host;  // final: every earlier call and this one have completed
+    });
+}
+
+lg_core_error lg_backend_sgd_step(lg_ctx* ctx, void* stream, const lg_tensor* w,
+                                  const lg_tensor* dw, float lr) {
+    return run_op([&] {
+        decode({w, dw});
+        if (!same_shape(dw, w)) core_fail(LG_CORE_SHAPE, "shapes differ");
+        const uint64_t n = numel(w);
+        all_f32({w, dw});
+        if (w->base == dw->base) core_fail(LG_CORE_ALIAS, "w and dw share storage");
+        packed({w, dw});
+        hipStream_t s = device_stream(ctx, stream);
+        if (n > 0) launch_sgd_step(ctx, s, dev<float>(w), dev<float>(dw), lr, n);
+    });
+}
+
+lg_core_error lg_backend_convert(lg_ctx* ctx, void* stream, const lg_tensor* x, const lg_tensor* y) {
+    return run_op([&] {
+        decode({x, y});
+        if (!same_shape(y, x)) core_fail(LG_CORE_SHAPE, "shapes differ");
+        const uint64_t n = numel(x);
+        const bool to_bf16 = x->dtype == LG_DTYPE_F32 && y->dtype == LG_DTYPE_BF16;
+        const bool to_f32 = x->dtype == LG_DTYPE_BF16 && y->dtype == LG_DTYPE_F32;
+        if (!to_bf16 && !to_f32) core_fail(LG_CORE_DTYPE, "convert needs (F32, BF16) or (BF16, F32)");
+        if (x->base == y->base) core_fail(LG_CORE_ALIAS, "x and y share storage");
+        packed({x, y});
+        hipStream_t s = device_stream(ctx, stream);
+        if (n > 0) launch_convert(ctx, s, to_bf16, x->base, y->base, n);
+    });
+}
+
+}  // extern "C"
 
 extern "C" lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_tensor* a,
                                          const lg_tensor* b, const lg_tensor* c, float alpha,

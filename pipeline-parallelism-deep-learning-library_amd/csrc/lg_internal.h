@@ -197,6 +197,25 @@ uint64_t perm_tile_workgroups(uint64_t total_tiles);
 
 }  // namespace lg
 
+namespace lg {
+// Backend training-op kernels (training_kernels.hip). Operands are dense, offset 0, n > 0.
+constexpr uint64_t MSE_MAX_GROUPS = 4096;  // workgroups of the MSE reduction, at most
+constexpr uint64_t MSE_MIN_CHUNK = 4096;   // elements per MSE workgroup, at least
+uint64_t mse_groups(uint64_t n, uint64_t* chunk);
+void launch_gelu(Context* ctx, hipStream_t s, const float* x, float* y, uint64_t n);
+void launch_gelu_backward(Context* ctx, hipStream_t s, const float* pre, const float* dy,
+                          float* dx, uint64_t n);
+void launch_add_bias(Context* ctx, hipStream_t s, const float* x, const float* b, float* y,
+                     uint64_t rows, uint64_t cols);
+void launch_bias_grad(Context* ctx, hipStream_t s, const float* dpre, float* db, uint32_t rows,
+                      uint32_t cols);
+// partial: mse_groups(n) floats; counter: one zeroed uint32; loss: one float (all device).
+void launch_mse_grad(Context* ctx, hipStream_t s, const float* y, const float* target, float* dy,
+                     uint64_t n, float* partial, uint32_t* counter, float* loss);
+void launch_sgd_step(Context* ctx, hipStream_t s, float* w, float* dw, float lr, uint64_t n);
+void launch_convert(Context* ctx, hipStream_t s, bool to_bf16, const void* x, void* y, uint64_t n);
+}  // namespace lg
+
 struct lg_ctx : lg::Context {};
 
 namespace lg {

@@ -84,6 +84,13 @@ SIGNATURES = {
     "lg_gemm_f32": (i32, [vp, F, VP, VP, F, VP]),
     "lg_gemm_nowait_f32": (i32, [vp, F, VP, VP, F, VP]),
     "lg_backend_gemm": (i32, [vp, vp, TP, TP, TP, F, F]),
+    "lg_backend_gelu": (i32, [vp, vp, TP, TP]),
+    "lg_backend_gelu_backward": (i32, [vp, vp, TP, TP, TP]),
+    "lg_backend_add_bias": (i32, [vp, vp, TP, TP, TP]),
+    "lg_backend_bias_grad": (i32, [vp, vp, TP, TP]),
+    "lg_backend_mse_grad": (i32, [vp, vp, TP, TP, TP, ctypes.POINTER(F)]),
+    "lg_backend_sgd_step": (i32, [vp, vp, TP, TP, F]),
+    "lg_backend_convert": (i32, [vp, vp, TP, TP]),
     "lg_plan_contract_f32": (i32, [F, VP, cp, VP, cp, F, VP, cp,
                                    ctypes.POINTER(lg_contract_plan)]),
     "lg_plan_gemm_f32": (i32, [F, VP, VP, F, VP, ctypes.POINTER(lg_contract_plan)]),

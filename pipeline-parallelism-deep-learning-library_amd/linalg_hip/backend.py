@@ -1,11 +1,12 @@
-"""The pipeline's tensor-backend surface for gemm on a HIP device.
+"""The pipeline's tensor-backend surface on a HIP device.
 
 Mirrors `linalg_core` (crates/core/src/lib.rs): `DType` (:10-32), `Error` (:42-53), `Tensor`
-(:55-61), the `Backend` trait's alloc / upload / download / sync / gemm (:103-164),
-`row_major_strides` (:275-283) and `transpose_matrix` (:285-296). `HipBackend.gemm` calls
-`lg_backend_gemm`, which checks operands in `CpuBackend::gemm`'s order
-(crates/cpu/src/lib.rs:203-250) and runs the contraction path's MFMA kernels; nothing runs on
-the host. A tensor's storage id is its device allocation's base address.
+(:55-61), the `Backend` trait (:103-255: alloc / upload / download / sync, gemm, gelu,
+gelu_backward, add_bias, bias_grad, mse_grad, sgd_step, convert), `row_major_strides`
+(:275-283) and `transpose_matrix` (:285-296). Every op calls its `lg_backend_*` entry point,
+which checks operands in `CpuBackend`'s order (crates/cpu/src/lib.rs:203-533) and runs a HIP
+kernel; nothing is computed on the host. A tensor's storage id is its device allocation's base
+address.
 """
 from __future__ import annotations
 
@@ -102,11 +103,26 @@ def transpose_matrix(t: Tensor) -> Tensor:
                   t.offset)
 
 
+def _refs(*tensors):
+    return [ctypes.byref(t.to_c()) for t in tensors]
+
+
 def gemm_checks(a: Tensor, b: Tensor, c: Tensor, alpha: float, beta: float) -> None:
     """Runs `lg_backend_gemm`'s operand checks with no context: raises the first check that
     fails, or `UnsupportedDevice` ("null context") when every check passes. Host only."""
-    _raise(N.lib().lg_backend_gemm(None, None, ctypes.byref(a.to_c()), ctypes.byref(b.to_c()),
-                                   ctypes.byref(c.to_c()), alpha, beta))
+    _raise(N.lib().lg_backend_gemm(None, None, *_refs(a, b, c), alpha, beta))
+
+
+def op_checks(op: str, *args) -> None:
+    """The same for the activation and training ops: `op` is "gelu", "gelu_backward",
+    "add_bias", "bias_grad", "mse_grad", "sgd_step" or "convert"; `args` are the op's tensors
+    followed by its scalar (`lr` for sgd_step). Host only."""
+    fn = getattr(N.lib(), f"lg_backend_{op}")
+    tensors = [a for a in args if isinstance(a, Tensor)]
+    scalars = [a for a in args if not isinstance(a, Tensor)]
+    if op == "mse_grad":
+        scalars = [ctypes.byref(ctypes.c_float(0.0))]
+    _raise(fn(None, None, *_refs(*tensors), *scalars))
 
 
 def _nbytes(dtype: DType, shape: Sequence[int]) -> int:
@@ -176,6 +192,40 @@ class HipBackend:
         _raise(N.lib().lg_backend_gemm(self.ctx.handle, None, ctypes.byref(a.to_c()),
                                        ctypes.byref(b.to_c()), ctypes.byref(c.to_c()), alpha,
                                        beta))
+
+    def _op(self, op: str, *args) -> None:
+        _raise(getattr(N.lib(), f"lg_backend_{op}")(self.ctx.handle, None, *args))
+
+    def gelu(self, x: Tensor, y: Tensor) -> None:
+        """`Backend::gelu` (crates/core/src/lib.rs:165-168)."""
+        self._op("gelu", *_refs(x, y))
+
+    def gelu_backward(self, pre: Tensor, dy: Tensor, dx: Tensor) -> None:
+        """`Backend::gelu_backward` (crates/core/src/lib.rs:170-180)."""
+        self._op("gelu_backward", *_refs(pre, dy, dx))
+
+    def add_bias(self, x: Tensor, b: Tensor, y: Tensor) -> None:
+        """`Backend::add_bias` (crates/core/src/lib.rs:182-191); `y` may be `x`."""
+        self._op("add_bias", *_refs(x, b, y))
+
+    def bias_grad(self, dpre: Tensor, db: Tensor) -> None:
+        """`Backend::bias_grad` (crates/core/src/lib.rs:193-201)."""
+        self._op("bias_grad", *_refs(dpre, db))
+
+    def mse_grad(self, y: Tensor, target: Tensor, dy: Tensor) -> float:
+        """`Backend::mse_grad` (crates/core/src/lib.rs:203-217): returns the loss once every
+        earlier call and this one have completed."""
+        loss = ctypes.c_float(0.0)
+        self._op("mse_grad", *_refs(y, target, dy), ctypes.byref(loss))
+        return loss.value
+
+    def sgd_step(self, w: Tensor, dw: Tensor, lr: float) -> None:
+        """`Backend::sgd_step` (crates/core/src/lib.rs:219-227)."""
+        self._op("sgd_step", *_refs(w, dw), lr)
+
+    def convert(self, x: Tensor, y: Tensor) -> None:
+        """`Backend::convert` (crates/core/src/lib.rs:229-236): F32 <-> BF16."""
+        self._op("convert", *_refs(x, y))
 
     def sync(self) -> None:
         try:

@@ -175,3 +175,87 @@ def test_non_finite_alpha_takes_the_general_kernel():
     for alpha in (math.inf, -math.inf, math.nan):
         assert C.plan_gemm(alpha, a, b, 0.0, c)["kind"] == "general"
     assert C.plan_gemm(3.0e38, a, b, 0.0, c)["kind"] == "tiled"
+
+
+# ---- training ops: crates/cpu/src/training.rs:291-372 and invariants.rs:503-520 ----------
+def op_kind(op, *args) -> str:
+    with pytest.raises(B.BackendError) as e:
+        B.op_checks(op, *args)
+    return e.value.kind
+
+
+def alias_of(t: B.Tensor, **kw) -> B.Tensor:
+    fields = dict(storage=t.storage, dtype=t.dtype, shape=list(t.shape), strides=list(t.strides),
+                  offset=t.offset)
+    fields.update(kw)
+    return B.Tensor(**fields)
+
+
+def test_training_op_errors_come_in_contract_order():
+    x, b, b_wrong = rm([2, 3]), rm([3]), rm([4])
+    h, hb = rm([2, 3], B.DType.BF16), rm([3], B.DType.BF16)
+    y = rm([2, 3])
+    odd = alias_of(y, strides=[1, 2])
+    # add_bias
+    assert op_kind("add_bias", h, b_wrong, y) == "Shape"
+    assert op_kind("add_bias", h, b, y) == "Dtype"
+    assert op_kind("add_bias", x, b, alias_of(b)) == "Shape"
+    assert op_kind("add_bias", x, alias_of(y), y) == "Shape"
+    assert op_kind("add_bias", x, alias_of(y, shape=[3], strides=[1]), y) == "Alias"
+    assert op_kind("add_bias", x, b, odd) == "UnsupportedLayout"
+    # bias_grad
+    db = rm([3])
+    assert op_kind("bias_grad", h, alias_of(b_wrong)) == "Shape"
+    assert op_kind("bias_grad", x, alias_of(hb)) == "Dtype"
+    assert op_kind("bias_grad", x, alias_of(x, shape=[3], strides=[1])) == "Alias"
+    assert op_kind("bias_grad", alias_of(x, strides=[1, 2]), db) == "UnsupportedLayout"
+    # mse_grad
+    empty = rm([0, 3])
+    assert op_kind("mse_grad", empty, empty, alias_of(empty)) == "Shape"
+    assert op_kind("mse_grad", x, b, y) == "Shape"
+    assert op_kind("mse_grad", h, x, y) == "Dtype"
+    assert op_kind("mse_grad", x, y, alias_of(y)) == "Alias"
+    assert op_kind("mse_grad", x, x, odd) == "UnsupportedLayout"
+    # sgd_step
+    w = rm([3])
+    assert op_kind("sgd_step", w, alias_of(x), 0.1) == "Shape"
+    assert op_kind("sgd_step", w, alias_of(hb), 0.1) == "Dtype"
+    assert op_kind("sgd_step", w, alias_of(w), 0.1) == "Alias"
+    assert op_kind("sgd_step", alias_of(w, offset=1), db, 0.1) == "UnsupportedLayout"
+    # convert
+    h_out = rm([2, 3], B.DType.BF16)
+    assert op_kind("convert", x, alias_of(hb)) == "Shape"
+    assert op_kind("convert", x, y) == "Dtype"
+    assert op_kind("convert", h, alias_of(h)) == "Dtype"
+    assert op_kind("convert", x, alias_of(x, dtype=B.DType.BF16)) == "Alias"
+    assert op_kind("convert", alias_of(x, strides=[1, 2]), h_out) == "UnsupportedLayout"
+    # gelu / gelu_backward (prepare_f32_row_major): Dtype, Shape, layout, storage.
+    f16 = rm([4], B.DType.F16)
+    assert op_kind("gelu", f16, rm([4])) == "Dtype"
+    assert op_kind("gelu", rm([4]), rm([5])) == "Shape"
+    assert op_kind("gelu", alias_of(rm([4]), strides=[2]), rm([4])) == "UnsupportedLayout"
+    short = rm([4])
+    short.storage = storage(12)
+    assert op_kind("gelu", short, rm([4])) == "Shape"
+    assert op_kind("gelu_backward", rm([4]), rm([4], B.DType.BF16), rm([4])) == "Dtype"
+    assert op_kind("gelu_backward", rm([4]), rm([4]), rm([2, 2])) == "Shape"
+    # Storage too short after the layout check: Shape.
+    tiny = rm([2, 3])
+    tiny.storage = storage(20)
+    assert op_kind("add_bias", tiny, b, y) == "Shape"
+    assert op_kind("sgd_step", rm([6]), alias_of(tiny, shape=[6], strides=[1]), 0.1) == "Shape"
+    # An undecodable dtype tag is a wire error everywhere.
+    assert op_kind("gelu", alias_of(x, dtype=7), y) == "Wire"
+
+
+def test_training_ops_pass_their_checks_on_valid_operands():
+    x, b, y = rm([2, 3]), rm([3]), rm([2, 3])
+    cases = [("gelu", x, y), ("gelu", x, alias_of(x)), ("gelu_backward", x, rm([2, 3]), y),
+             ("add_bias", x, b, y), ("add_bias", x, b, alias_of(x)), ("bias_grad", x, b),
+             ("bias_grad", rm([0, 3]), b), ("mse_grad", x, rm([2, 3]), alias_of(x)),
+             ("mse_grad", x, alias_of(x), y), ("sgd_step", x, y, 0.5),
+             ("convert", x, rm([2, 3], B.DType.BF16)), ("convert", rm([2, 3], B.DType.BF16), x)]
+    for op, *args in cases:
+        with pytest.raises(B.BackendError, match="null context") as e:
+            B.op_checks(op, *args)
+        assert e.value.kind == "UnsupportedDevice", op
