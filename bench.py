@@ -139,6 +139,45 @@ def bench_copy(ctx, events, pool, L, P, n, args):
     return 2.0 * n * 4 / (ms * 1e-3) / 1e9
 
 
+def bench_train_ops(events, args, timed_fn):
+    """The Backend activation and training ops at the config-5 layer shape [4096, 16384]
+    (Y = X.W of the 1F1B linear step): each op's algorithmic bytes / mean kernel time."""
+    from linalg_hip import backend as B
+    hb = B.HipBackend(0)
+    rows, cols = 4096, 16384
+    n = rows * cols
+    g = np.random.Generator(np.random.PCG64(21))
+    a = (g.standard_normal(n) * 0.5).astype(np.float32)
+    b = (g.standard_normal(n) * 0.5).astype(np.float32)
+    x = hb.upload_f32([rows, cols], a)
+    t = hb.upload_f32([rows, cols], b)
+    y = hb.alloc(B.DType.F32, [rows, cols])
+    z = hb.alloc(B.DType.F32, [rows, cols])
+    bias = hb.upload_f32([cols], a[:cols])
+    db = hb.alloc(B.DType.F32, [cols])
+    h = hb.alloc(B.DType.BF16, [rows, cols])
+    f4, f2 = 4 * n, 2 * n
+    ops = [
+        ("gelu", lambda: hb.gelu(x, y), 2 * f4, "gelu_f32<true>"),
+        ("gelu_backward", lambda: hb.gelu_backward(x, t, y), 3 * f4, "gelu_backward_f32<true>"),
+        ("add_bias", lambda: hb.add_bias(x, bias, y), 2 * f4 + 4 * cols, "add_bias_f32<true>"),
+        ("bias_grad", lambda: hb.bias_grad(x, db), f4 + 8 * cols, "bias_grad_f32"),
+        ("mse_grad", lambda: hb.mse_grad(x, t, z), 3 * f4, "mse_grad_f32 (synchronous)"),
+        ("sgd_step", lambda: hb.sgd_step(y, z, 1e-3), 4 * f4, "sgd_step_f32<true>"),
+        ("convert_f32_bf16", lambda: hb.convert(x, h), f4 + f2, "convert_f32_bf16<true>"),
+        ("convert_bf16_f32", lambda: hb.convert(h, y), f2 + f4, "convert_bf16_f32<true>"),
+    ]
+    out = {}
+    for name, fn, nbytes, kernel in ops:
+        ms = timed_fn(hb.ctx, events, fn, args.steps, args.warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": ms, "gbs": gbs, "frac": gbs / PEAK_GBS, "bytes": nbytes,
+                     "kernel": kernel}
+    hb.close()
+    out["_shape"] = [rows, cols]
+    return out
+
+
 def traffic_from_profile(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic_<name>.txt)."""
     p = REPO / "profiles" / f"traffic_{name}.txt"
@@ -204,7 +243,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default=None,
-                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy")
+                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, train")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -273,7 +312,9 @@ def main() -> int:
                                   [512, 1024, 256], [2, 0, 1], 4, args))
     run("copy", lambda: {"name": "plain 128-bit copy 512 MiB", "gbs": bench_copy(ctx, events, pool,
                                                                                  L, P, 1 << 27, args)})
+    run("train", lambda: bench_train_ops(events, args, timed))
 
+    train = results.pop("train", None)
     gemm_host = results.get("gemm4096", {}).pop("_host", None)
     perm_host = results.get("c2b", {}).pop("_host", None)
     for r in results.values():
@@ -315,6 +356,15 @@ def main() -> int:
                                         "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
                                         "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
                            "cpu_baseline": cpu["permute"] if cpu else None}
+    if train:
+        shape = train.pop("_shape")
+        line["train_ops"] = {
+            "workload": f"Backend ops on f32 [{shape[0]}, {shape[1]}] (the config-5 layer "
+                        "activation), HBM roofline, algorithmic bytes = every operand read and "
+                        "written once",
+            "peak_gbs": PEAK_GBS,
+            "ops": {k_: {kk: (round(v, 4) if isinstance(v, float) else v) for kk, v in r.items()}
+                    for k_, r in train.items()}}
     line["configs"] = {k_: {kk: (round(v, 4) if isinstance(v, float) else v)
                             for kk, v in r.items()} for k_, r in results.items()}
     print(json.dumps(line), flush=True)

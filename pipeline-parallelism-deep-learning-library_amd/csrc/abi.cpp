@@ -198,6 +198,8 @@ void lg_ctx_destroy(lg_ctx* ctx) {
     if (ctx == nullptr) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->mse_scratch != nullptr) (void)hipFree(ctx->mse_scratch);
+    if (ctx->mse_host != nullptr) (void)hipHostFree(ctx->mse_host);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }

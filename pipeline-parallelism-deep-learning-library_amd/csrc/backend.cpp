@@ -284,31 +284,24 @@ lg_core_error lg_backend_mse_grad(lg_ctx* ctx, void* stream, const lg_tensor* y,
         packed({y, target, dy});
         if (loss == nullptr) core_fail(LG_CORE_SHAPE, "null loss pointer");
         hipStream_t s = device_stream(ctx, stream);
-        uint64_t chunk = 0;
-        const uint64_t groups = mse_groups(n, &chunk);
-        // Scratch: partial[groups], then the counter, then the loss; stream-ordered.
-        const size_t bytes = (groups + 2) * sizeof(float);
-        void* scratch = nullptr;
-        check_hip(hipMallocAsync(&scratch, bytes, s), "hipMallocAsync");
-        float* partial = static_cast<float*>(scratch);
-        uint32_t* counter = reinterpret_cast<uint32_t*>(partial + groups);
-        float* dloss = partial + groups + 1;
-        float host = 0.0f;
-        hipError_t e = hipMemsetAsync(counter, 0, sizeof(uint32_t), s);
-        if (e == hipSuccess) {
-            try {
-                launch_mse_grad(ctx, s, dev<const float>(y), dev<const float>(target), dev<float>(dy), n,
-                                partial, counter, dloss);
-            } catch (...) {
-                (void)hipFreeAsync(scratch, s);
-                throw;
-            }
-            e = hipMemcpyAsync(&host, dloss, sizeof(float), hipMemcpyDeviceToHost, s);
+        std::lock_guard<std::mutex> hold(ctx->mse_lock);
+        // Scratch: partial[MSE_MAX_GROUPS], then the counter, then the loss.
+        if (ctx->mse_scratch == nullptr) {
+            check_hip(hipMalloc(&ctx->mse_scratch, (MSE_MAX_GROUPS + 2) * sizeof(float)), "hipMalloc");
         }
-        const hipError_t f = hipFreeAsync(scratch, s);
-        check_hip(e, "mse_grad");
-        check_hip(f, "hipFreeAsync");
+        if (ctx->mse_host == nullptr) {
+            check_hip(hipHostMalloc(reinterpret_cast<void**>(&ctx->mse_host), sizeof(float)), "hipHostMalloc");
+        }
+        float* partial = static_cast<float*>(ctx->mse_scratch);
+        uint32_t* counter = reinterpret_cast<uint32_t*>(partial + MSE_MAX_GROUPS);
+        float* dloss = partial + MSE_MAX_GROUPS + 1;
+        check_hip(hipMemsetAsync(counter, 0, sizeof(uint32_t), s), "hipMemsetAsync");
+        launch_mse_grad(ctx, s, dev<const float>(y), dev<const float>(target), dev<float>(dy), n,
+                        partial, counter, dloss);
+        check_hip(hipMemcpyAsync(ctx->mse_host, dloss, sizeof(float), hipMemcpyDeviceToHost, s),
+                  "hipMemcpyAsync");
         check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+        const float host = *ctx->mse_host;
         *loss = host;  // final: every earlier call and this one have completed
     });
 }

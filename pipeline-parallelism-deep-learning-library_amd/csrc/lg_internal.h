@@ -7,6 +7,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -65,6 +66,12 @@ struct Context {
     hipStream_t stream = nullptr;
     std::atomic<uint64_t> launches{0};
     std::atomic<const char*> names[256];
+    // The MSE reduction's scratch (partials, ticket counter, loss) and the pinned host word
+    // the loss is read back into; made on first use, freed with the context. mse_grad holds
+    // mse_lock from its launch until the loss is back, so concurrent calls take turns.
+    std::mutex mse_lock;
+    void* mse_scratch = nullptr;
+    float* mse_host = nullptr;
 };
 void note_launch(Context* ctx, const char* name);
 void set_last_error(const std::string& msg);
@@ -199,7 +206,7 @@ uint64_t perm_tile_workgroups(uint64_t total_tiles);
 
 namespace lg {
 // Backend training-op kernels (training_kernels.hip). Operands are dense, offset 0, n > 0.
-constexpr uint64_t MSE_MAX_GROUPS = 4096;  // workgroups of the MSE reduction, at most
+constexpr uint64_t MSE_MAX_GROUPS = 256;   // workgroups of the MSE reduction, at most
 constexpr uint64_t MSE_MIN_CHUNK = 4096;   // elements per MSE workgroup, at least
 uint64_t mse_groups(uint64_t n, uint64_t* chunk);
 void launch_gelu(Context* ctx, hipStream_t s, const float* x, float* y, uint64_t n);

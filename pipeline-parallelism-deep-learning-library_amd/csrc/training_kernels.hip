@@ -19,7 +19,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int THREADS = 256;
-constexpr uint64_t GRID_CAP = 8192;
+// One 128-bit vector per thread for every tensor up to 2^30 vectors: many short-lived
+// workgroups keep more loads in flight than a grid-stride loop over a capped grid.
+constexpr uint64_t GRID_CAP = 1u << 20;
 
 // Abramowitz & Stegun 7.1.26 (max |error| 1.5e-7 on erf), with the coefficients rounded to
 // f32: 0.254829592, -0.284496736, 1.421413741, -1.453152027, 1.061405429, p = 0.3275911.
@@ -110,34 +112,78 @@ __global__ __launch_bounds__(THREADS) void add_bias_f32(const float* x, const fl
 }
 
 // db[j] = db[j] + s[j], s[j] = dpre[0][j] + dpre[1][j] + ... in row order: the reference's
-// sequential column sum, one lane per column (loads coalesce across lanes). UNROLL loads are
-// issued before they are added, in order, so each lane keeps UNROLL loads in flight.
-constexpr int BIAS_UNROLL = 16;
+// sequential column sum, bit for bit. The dependency chain runs down each column, so the
+// loads are decoupled from it: a workgroup owns BG_COLS columns; all four waves stream blocks
+// of BG_ROWS rows into a double-buffered LDS tile (the next block's loads are in flight while
+// the current one is summed), and wave 0 -- one lane per column -- adds the block's rows in
+// order. One workgroup per 64 columns keeps 64 KB of loads in flight per CU (128 KB of LDS).
+constexpr int BG_COLS = 64;
+constexpr int BG_ROWS = 256;
+constexpr int BG_LOADS = BG_ROWS * BG_COLS / 4 / THREADS;  // 128-bit loads per thread per block
+static_assert(BG_LOADS * THREADS * 4 == BG_ROWS * BG_COLS, "block must split evenly");
+
+template <bool VEC>
 __global__ __launch_bounds__(THREADS) void bias_grad_f32(const float* dpre, float* db,
                                                          uint32_t rows, uint32_t cols) {
-    const uint32_t j = blockIdx.x * THREADS + threadIdx.x;
-    if (j >= cols) return;
-    const float* p = dpre + j;
+    __shared__ f32x4 tile[2][BG_ROWS * BG_COLS / 4];
+    const int tid = threadIdx.x;
+    const uint32_t c0 = blockIdx.x * BG_COLS;
+    const uint32_t nblk = (rows + BG_ROWS - 1) / BG_ROWS;
+    f32x4 r[BG_LOADS];
+    // Element (row, col) of block b: thread t's i-th vector covers row (i*THREADS+t) / 16,
+    // columns 4*((i*THREADS+t) % 16) .. +3 of the workgroup's 64.
+    auto fetch = [&](uint32_t b) {
+#pragma unroll
+        for (int i = 0; i < BG_LOADS; ++i) {
+            const int v = i * THREADS + tid;
+            const uint32_t row = b * BG_ROWS + v / (BG_COLS / 4);
+            const uint32_t col = c0 + (v % (BG_COLS / 4)) * 4;
+            const float* p = dpre + static_cast<uint64_t>(row) * cols + col;
+            if (VEC && row < rows && col + 4 <= cols) {
+                r[i] = *reinterpret_cast<const f32x4*>(p);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[i][e] = (row < rows && col + e < cols) ? p[e] : 0.0f;
+            }
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < BG_LOADS; ++i) tile[buf][i * THREADS + tid] = r[i];
+    };
+    fetch(0);
+    stash(0);
+    __syncthreads();
     float s = 0.0f;
-    uint32_t r = 0;
-    for (; r + BIAS_UNROLL <= rows; r += BIAS_UNROLL) {
-        float v[BIAS_UNROLL];
-#pragma unroll
-        for (int u = 0; u < BIAS_UNROLL; ++u) v[u] = p[static_cast<uint64_t>(r + u) * cols];
-#pragma unroll
-        for (int u = 0; u < BIAS_UNROLL; ++u) s = s + v[u];
+    const float* lane_col = reinterpret_cast<const float*>(tile[0]) + tid;  // wave 0 only
+    for (uint32_t b = 0; b < nblk; ++b) {
+        const int buf = b & 1;
+        if (b + 1 < nblk) fetch(b + 1);
+        if (tid < BG_COLS) {
+            const uint32_t n = min(static_cast<uint32_t>(BG_ROWS), rows - b * BG_ROWS);
+            const float* col = lane_col + buf * BG_ROWS * BG_COLS;
+            for (uint32_t i = 0; i < n; ++i) s = s + col[i * BG_COLS];
+        }
+        if (b + 1 < nblk) stash(buf ^ 1);
+        __syncthreads();
     }
-    for (; r < rows; ++r) s = s + p[static_cast<uint64_t>(r) * cols];
-    db[j] = db[j] + s;
+    const uint32_t j = c0 + tid;
+    if (tid < BG_COLS && j < cols) db[j] = db[j] + s;
 }
 
-// MSE: d = y - target; dy = (2*d) / n; loss = (sum d*d) / n, in one launch. Workgroup g owns
+// MSE: d = y - target; dy = (2*d) / n; loss = (sum d*d) / n, in one launch. At most
+// MSE_MAX_GROUPS workgroups: each pays one device-scope release (an L2 write-back on this
+// multi-XCD part), which measured 0.1 us apiece when 4096 workgroups issued them. Workgroup g owns
 // the contiguous run [g*chunk, (g+1)*chunk); each lane sums its strided share in index order,
 // the 256 lane sums meet in a fixed LDS tree, and the workgroup's sum goes to partial[g]. The
 // workgroup that finishes last (ticket from a device-wide counter) adds partial[0..G) in a
-// fixed order and writes the loss, so the summation order depends only on n. dy may be y.
+// fixed order and writes the loss, so the summation order depends only on n (VEC, 128-bit
+// accesses, is chosen by n % 4 and alignment alone). dy may be y.
 // The counter starts at zero (the host clears it before the launch); nothing waits on another
 // workgroup, so no schedule can hang.
+constexpr int MSE_UNROLL = 4;
+
+template <bool VEC>
 __global__ __launch_bounds__(THREADS) void mse_grad_f32(const float* y, const float* target,
                                                         float* dy, uint64_t n, uint64_t chunk,
                                                         float nf, float* partial,
@@ -148,10 +194,40 @@ __global__ __launch_bounds__(THREADS) void mse_grad_f32(const float* y, const fl
     const uint64_t lo = static_cast<uint64_t>(blockIdx.x) * chunk;
     const uint64_t hi = lo + chunk < n ? lo + chunk : n;
     float s = 0.0f;
-    for (uint64_t i = lo + threadIdx.x; i < hi; i += THREADS) {
-        const float d = y[i] - target[i];
-        s = s + d * d;
-        dy[i] = (2.0f * d) / nf;
+    if (VEC) {
+        // chunk and lo are multiples of 4: lane t takes vectors t, t + 256, ... of the run and
+        // adds the four squares of each in index order; MSE_UNROLL vectors' loads are issued
+        // before the first is used.
+        const f32x4* yv = reinterpret_cast<const f32x4*>(y + lo);
+        const f32x4* tv = reinterpret_cast<const f32x4*>(target + lo);
+        f32x4* dv = reinterpret_cast<f32x4*>(dy + lo);
+        const uint64_t nv = (hi - lo) / 4;
+        auto one = [&](f32x4 a, f32x4 b, uint64_t i) {
+            const f32x4 d = a - b;
+            s = s + d[0] * d[0];
+            s = s + d[1] * d[1];
+            s = s + d[2] * d[2];
+            s = s + d[3] * d[3];
+            dv[i] = (2.0f * d) / nf;
+        };
+        uint64_t i = threadIdx.x;
+        for (; i + (MSE_UNROLL - 1) * THREADS < nv; i += MSE_UNROLL * THREADS) {
+            f32x4 a[MSE_UNROLL], b[MSE_UNROLL];
+#pragma unroll
+            for (int u = 0; u < MSE_UNROLL; ++u) {
+                a[u] = yv[i + u * THREADS];
+                b[u] = tv[i + u * THREADS];
+            }
+#pragma unroll
+            for (int u = 0; u < MSE_UNROLL; ++u) one(a[u], b[u], i + u * THREADS);
+        }
+        for (; i < nv; i += THREADS) one(yv[i], tv[i], i);
+    } else {
+        for (uint64_t i = lo + threadIdx.x; i < hi; i += THREADS) {
+            const float d = y[i] - target[i];
+            s = s + d * d;
+            dy[i] = (2.0f * d) / nf;
+        }
     }
     red[threadIdx.x] = s;
     __syncthreads();
@@ -296,16 +372,21 @@ void launch_add_bias(Context* ctx, hipStream_t s, const float* x, const float* b
 
 void launch_bias_grad(Context* ctx, hipStream_t s, const float* dpre, float* db, uint32_t rows,
                       uint32_t cols) {
-    const uint32_t g = (cols + THREADS - 1) / THREADS;
-    hipLaunchKernelGGL(bias_grad_f32, dim3(g), dim3(THREADS), 0, s, dpre, db, rows, cols);
+    const uint32_t g = (cols + BG_COLS - 1) / BG_COLS;
+    if (cols % 4 == 0 && aligned(dpre, 16)) {
+        hipLaunchKernelGGL(bias_grad_f32<true>, dim3(g), dim3(THREADS), 0, s, dpre, db, rows, cols);
+    } else {
+        hipLaunchKernelGGL(bias_grad_f32<false>, dim3(g), dim3(THREADS), 0, s, dpre, db, rows, cols);
+    }
     after_launch(ctx, "bias_grad_f32");
 }
 
 uint64_t mse_groups(uint64_t n, uint64_t* chunk) {
-    // At least 4096 elements per workgroup, at most 4096 workgroups; shape-only, so the
-    // summation order is a function of n alone.
+    // At least MSE_MIN_CHUNK elements per workgroup, at most MSE_MAX_GROUPS workgroups;
+    // shape-only, so the summation order is a function of n alone.
     uint64_t c = (n + MSE_MAX_GROUPS - 1) / MSE_MAX_GROUPS;
     if (c < MSE_MIN_CHUNK) c = MSE_MIN_CHUNK;
+    c = (c + 3) / 4 * 4;  // whole 128-bit vectors per workgroup
     *chunk = c;
     return (n + c - 1) / c;
 }
@@ -315,8 +396,13 @@ void launch_mse_grad(Context* ctx, hipStream_t s, const float* y, const float* t
     uint64_t chunk = 0;
     const uint64_t g = mse_groups(n, &chunk);
     const float nf = static_cast<float>(n);
-    hipLaunchKernelGGL(mse_grad_f32, dim3(static_cast<uint32_t>(g)), dim3(THREADS), 0, s, y, target,
-                       dy, n, chunk, nf, partial, counter, loss);
+    if (n % 4 == 0 && aligned(y, 16) && aligned(target, 16) && aligned(dy, 16)) {
+        hipLaunchKernelGGL(mse_grad_f32<true>, dim3(static_cast<uint32_t>(g)), dim3(THREADS), 0, s,
+                           y, target, dy, n, chunk, nf, partial, counter, loss);
+    } else {
+        hipLaunchKernelGGL(mse_grad_f32<false>, dim3(static_cast<uint32_t>(g)), dim3(THREADS), 0, s,
+                           y, target, dy, n, chunk, nf, partial, counter, loss);
+    }
     after_launch(ctx, "mse_grad_f32");
 }
 
