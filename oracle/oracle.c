@@ -259,7 +259,7 @@ void oracle_contract_f64(float alpha_f, float beta_f, uint32_t n_free, const uin
  * ---------------------------------------------------------------------------------------- */
 
 /* The f32 spellings of A&S 7.1.26's coefficients and 1/sqrt(2 pi) the reference asserts
- * (crates/cpu/src/lib.rs:845-857): 0.2548296, 0.28449672, 1.4214138, 1.4531521, 1.0614054,
+ * (crates/cpu/src/lib.rs:846-853): 0.2548296, 0.28449672, 1.4214138, 1.4531521, 1.0614054,
  * 0.3989423. */
 static const float ERF_A1 = 0.2548296f;
 static const float ERF_A2 = 0.28449672f;

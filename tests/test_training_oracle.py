@@ -1,7 +1,7 @@
 """Pins the oracle's restatement of the CpuBackend activation and training ops (CPU only).
 
 Each check is one the reference itself makes, or one the mathematics fixes:
-* the A&S 7.1.26 constants carry the bit patterns crates/cpu/src/lib.rs:845-857 asserts;
+* the A&S 7.1.26 constants carry the bit patterns crates/cpu/src/lib.rs:846-853 asserts;
 * GELU and its derivative lie within 1e-6 of the normal-cdf definition on the reference's
   sample list (crates/cpu/src/invariants.rs:462-500), here against math.erf in f64;
 * add_bias / bias_grad / mse_grad / sgd_step equal the sequential f32 loops and lie within
