@@ -33,6 +33,7 @@ sys.path.insert(0, str(REPO))
 METRIC = "contraction TFLOP/s (% fp32 MFMA peak); permute GB/s (% HBM peak)"
 PEAK_TFLOPS = 157.3     # MI355X dense fp32 MFMA
 PEAK_GBS = 8000.0       # MI355X HBM3E
+PEAK_F64_TFLOPS = 78.6  # MI355X dense fp64 MFMA
 
 
 class HipEvents:
@@ -139,6 +140,27 @@ def bench_copy(ctx, events, pool, L, P, n, args):
     return 2.0 * n * 4 / (ms * 1e-3) / 1e9
 
 
+def bench_gemm_f16(ctx, events, pool, L, C, m, n, k, args):
+    """f16 contraction (each output rounded once from an f64 dot on the f64 matrix cores):
+    TFLOP/s against the 78.6 TFLOP/s f64 MFMA peak the kernel runs on."""
+    g = np.random.Generator(np.random.PCG64(31))
+    a = pool.alloc("f16", m * k)
+    b = pool.alloc("f16", k * n)
+    c = pool.alloc("f16", m * n)
+    a.write(g.uniform(-1, 1, m * k).astype(np.float16))
+    b.write(g.uniform(-1, 1, k * n).astype(np.float16))
+    av = L.TensorView.row_major(a, 0, [m, k], "f16")
+    bv = L.TensorView.row_major(b, 0, [k, n], "f16")
+    cv = L.TensorView.row_major(c, 0, [m, n], "f16")
+    plan = C.plan_gemm(1.0, av, bv, 0.0, cv)
+    ms = timed(ctx, events, lambda: C.encode_gemm(ctx, ctx.queue, 1.0, av, bv, 0.0, cv),
+               args.steps, args.warmup)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"name": f"f16 gemm {m}x{n}x{k} (f64 accumulation, one f16 rounding)", "ms": ms,
+            "tflops": tf, "frac_f64_mfma": tf / PEAK_F64_TFLOPS,
+            "plan": {k_: plan[k_] for k_ in ("kind", "workgroups")}}
+
+
 def bench_train_ops(events, args, timed_fn):
     """The Backend activation and training ops at the config-5 layer shape [4096, 16384]
     (Y = X.W of the 1F1B linear step): each op's algorithmic bytes / mean kernel time."""
@@ -243,7 +265,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default=None,
-                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, train")
+                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, train, f16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -313,6 +335,7 @@ def main() -> int:
     run("copy", lambda: {"name": "plain 128-bit copy 512 MiB", "gbs": bench_copy(ctx, events, pool,
                                                                                  L, P, 1 << 27, args)})
     run("train", lambda: bench_train_ops(events, args, timed))
+    run("f16", lambda: bench_gemm_f16(ctx, events, pool, L, C, 4096, 4096, 4096, args))
 
     train = results.pop("train", None)
     gemm_host = results.get("gemm4096", {}).pop("_host", None)

@@ -185,6 +185,27 @@ lg_status lg_gemm_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view*
 lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b,
                              float beta, const lg_view* c);
 
+/* The same five entry points for half operands: contract / gemm / gemm_nowait instantiated at
+ * `T = half::f16` (src/ops/contraction.rs:22-32,147-162,1036-1130). Views are in f16
+ * elements (2 bytes, 2-byte aligned base); alpha and beta stay f32. Validation, label and
+ * alias rules are the f32 ones. Each output is the exact-product dot rounded ONCE to f16:
+ * products of halves are exact in f64 and summed in f64 (the reference sums them in
+ * double-float f32 and rounds once, shaders/contraction.metal:444-678); alpha*acc and beta*C
+ * add in f64 and round to nearest even. beta*C alone (alpha = 0 or K = 0) is the exact product
+ * rounded once (contract_scale_f16, shaders/contraction.metal:730-756). */
+lg_status lg_encode_contract_f16(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                 const char* a_labels, const lg_view* b, const char* b_labels,
+                                 float beta, const lg_view* c, const char* c_labels);
+lg_status lg_contract_f16(lg_ctx* ctx, float alpha, const lg_view* a, const char* a_labels,
+                          const lg_view* b, const char* b_labels, float beta, const lg_view* c,
+                          const char* c_labels);
+lg_status lg_encode_gemm_f16(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                             const lg_view* b, float beta, const lg_view* c);
+lg_status lg_gemm_f16(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b, float beta,
+                      const lg_view* c);
+lg_status lg_gemm_nowait_f16(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b,
+                             float beta, const lg_view* c);
+
 /* ---------------------------------------------------------------------------------------
  * Backend-style gemm: linalg_core::Backend::gemm (crates/core/src/lib.rs:143-164)
  * ------------------------------------------------------------------------------------- */
@@ -323,6 +344,13 @@ lg_status lg_plan_contract_f32(float alpha, const lg_view* a, const char* a_labe
                                const lg_view* b, const char* b_labels, float beta,
                                const lg_view* c, const char* c_labels, lg_contract_plan* out);
 lg_status lg_plan_gemm_f32(float alpha, const lg_view* a, const lg_view* b, float beta,
+                           const lg_view* c, lg_contract_plan* out);
+/* The plans of the f16 entry points: kinds EMPTY, ZERO, SCALE, TILED (the f64 matrix-core
+ * tile kernel, a 64x64 tile per workgroup, 16-bit strided loads) or GENERAL. */
+lg_status lg_plan_contract_f16(float alpha, const lg_view* a, const char* a_labels,
+                               const lg_view* b, const char* b_labels, float beta,
+                               const lg_view* c, const char* c_labels, lg_contract_plan* out);
+lg_status lg_plan_gemm_f16(float alpha, const lg_view* a, const lg_view* b, float beta,
                            const lg_view* c, lg_contract_plan* out);
 
 /* Permutation plan (encode_gather's path choice, src/ops/permutation.rs:200-268). */

@@ -275,3 +275,54 @@ def bf16_to_f32(h) -> np.ndarray:
     y = np.empty(h.shape, dtype=np.uint32)
     lib().oracle_bf16_to_f32(h.ctypes.data, y.ctypes.data, h.size)
     return y.view(np.float32)
+
+
+# ---- f16 contraction: the exact result rounded once ----------------------------------------
+def f16_round_exact(x) -> int:
+    """Bits of the f16 nearest the exact rational `x` (fractions.Fraction or int), ties to
+    even, overflow to infinity, subnormals kept: the single rounding the reference's f16 path
+    performs from its double-float dot (shaders/contraction.metal:575-607)."""
+    from fractions import Fraction
+    x = Fraction(x)
+    if x == 0:
+        return 0
+    sign = 0x8000 if x < 0 else 0
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    elif Fraction(2) ** (e + 1) <= a:
+        e += 1
+    quantum = Fraction(2) ** (max(e, -14) - 10)
+    q = a / quantum
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    value = n * quantum
+    if value >= 65536:
+        return sign | 0x7C00
+    return sign | int(np.float16(float(value)).view(np.uint16))
+
+
+def contract_exact_f16(alpha, a, b, beta, c) -> np.ndarray:
+    """Exact C = alpha*A.B + beta*C for dense 2-D f16 arrays, each element rounded once to
+    f16 (returned as uint16 bits). Test sizes only: Python rationals."""
+    from fractions import Fraction
+    a = np.asarray(a, np.float16)
+    b = np.asarray(b, np.float16)
+    c = np.asarray(c, np.float16)
+    m, k = a.shape
+    n = b.shape[1]
+    fa = [[Fraction(float(v)) for v in row] for row in a]
+    fb = [[Fraction(float(v)) for v in row] for row in b]
+    al, be = Fraction(float(np.float32(alpha))), Fraction(float(np.float32(beta)))
+    out = np.zeros((m, n), np.uint16)
+    for i in range(m):
+        for j in range(n):
+            s = sum((fa[i][t] * fb[t][j] for t in range(k)), Fraction(0)) if alpha != 0 else 0
+            v = al * s
+            if beta != 0:
+                v += be * Fraction(float(c[i, j]))
+            out[i, j] = f16_round_exact(v)
+    return out

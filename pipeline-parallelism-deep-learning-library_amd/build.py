@@ -27,6 +27,7 @@ SOURCES = [
     "contraction.cpp",
     "permutation.cpp",
     "contraction_kernels.hip",
+    "contraction_f16_kernels.hip",
     "permutation_kernels.hip",
     "training_kernels.hip",
 ]

@@ -110,8 +110,9 @@ void validate(const View& v, uint32_t elem_bytes) {
                      fmt_vec(v.strides));
     }
     if (v.base == 0) fail_invalid("null buffer base");
-    // Every element type here has 4-byte alignment (f32, u32, i32, [f32; 2]).
-    if (v.base % 4 != 0) fail_invalid("buffer base is misaligned for the element type");
+    // Alignment of the element type: 2 bytes for f16, 4 for f32, u32, i32 and [f32; 2].
+    const uint32_t align = elem_bytes < 4 ? elem_bytes : 4;
+    if (v.base % align != 0) fail_invalid("buffer base is misaligned for the element type");
     const uint64_t capacity = v.bytes / elem_bytes;
     if (v.is_empty()) {
         if (v.offset <= capacity) return;

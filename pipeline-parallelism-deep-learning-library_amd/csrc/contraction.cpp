@@ -391,11 +391,96 @@ Axes4 pack(const std::vector<Axis>& axes, char which) {
 
 struct Plan {
     lg_contract_plan info{};
+    bool half = false;  // f16 operands: the h* argument blocks below are the live ones
     GemmArgs gemm{};
     ReduceArgs reduce{};
     GeneralArgs general{};
     FillArgs fill{};
+    GemmHalfArgs hgemm{};
+    GeneralHalfArgs hgeneral{};
+    FillHalfArgs hfill{};
 };
+
+// The f16 plans: the same kinds, on the f16 kernels. No split-K: one f64 tile per output block.
+void plan_half(const View& a, const View& b, const View& c, const Merged& mg, float alpha,
+               float beta, bool reads_inputs, Plan& p) {
+    lg_contract_plan& info = p.info;
+    p.half = true;
+    uint16_t* cptr = reinterpret_cast<uint16_t*>(c.base) + c.offset;
+    if (!reads_inputs) {
+        info.kind = beta == 0.0f ? LG_PLAN_ZERO : LG_PLAN_SCALE;
+        FillHalfArgs& f = p.hfill;
+        f.c = cptr;
+        f.count = mg.batch_n * mg.m_n * mg.n_n;
+        f.m = fit32(mg.m_n, "M");
+        f.n = fit32(mg.n_n, "N");
+        f.batch = fit32(mg.batch_n, "batch");
+        f.beta = beta;
+        f.c_batch = pack(mg.batch, 'c');
+        f.c_m = pack(mg.m, 'c');
+        f.c_n = pack(mg.n, 'c');
+        info.workgroups = (f.count + 255) / 256;
+        return;
+    }
+    const uint32_t m = fit32(mg.m_n, "M"), n = fit32(mg.n_n, "N"), k = fit32(mg.k_n, "K"),
+                   batch = fit32(mg.batch_n, "batch");
+    const uint16_t* aptr = reinterpret_cast<const uint16_t*>(a.base) + a.offset;
+    const uint16_t* bptr = reinterpret_cast<const uint16_t*>(b.base) + b.offset;
+    const bool single = mg.batch.size() == 1 && mg.m.size() == 1 && mg.n.size() == 1 &&
+                        mg.k.size() == 1;
+    info.a_mode = LG_LOAD_STRIDED;
+    info.b_mode = LG_LOAD_STRIDED;
+    if (!single) {
+        info.kind = LG_PLAN_GENERAL;
+        GeneralHalfArgs& g = p.hgeneral;
+        g.a = aptr;
+        g.b = bptr;
+        g.c = cptr;
+        g.m = m;
+        g.n = n;
+        g.k = k;
+        g.batch = batch;
+        g.alpha = alpha;
+        g.beta = beta;
+        g.a_batch = pack(mg.batch, 'a');
+        g.a_m = pack(mg.m, 'a');
+        g.a_k = pack(mg.k, 'a');
+        g.b_batch = pack(mg.batch, 'b');
+        g.b_n = pack(mg.n, 'b');
+        g.b_k = pack(mg.k, 'b');
+        g.c_batch = pack(mg.batch, 'c');
+        g.c_m = pack(mg.m, 'c');
+        g.c_n = pack(mg.n, 'c');
+        info.workgroups = (mg.batch_n * mg.m_n * mg.n_n + 255) / 256;
+        return;
+    }
+    const Axis &ab = mg.batch[0], &am = mg.m[0], &an = mg.n[0], &ak = mg.k[0];
+    GemmHalfArgs& t = p.hgemm;
+    t.a = aptr;
+    t.b = bptr;
+    t.c = cptr;
+    t.a_sb = sfit(ab.a, "A batch stride");
+    t.a_sm = sfit(am.a, "A M stride");
+    t.a_sk = sfit(ak.a, "A K stride");
+    t.b_sb = sfit(ab.b, "B batch stride");
+    t.b_sn = sfit(an.b, "B N stride");
+    t.b_sk = sfit(ak.b, "B K stride");
+    t.c_sb = sfit(ab.c, "C batch stride");
+    t.c_sm = sfit(am.c, "C M stride");
+    t.c_sn = sfit(an.c, "C N stride");
+    t.m = m;
+    t.n = n;
+    t.k = k;
+    t.batch = batch;
+    t.tiles_m = (m + HGEMM_BM - 1) / HGEMM_BM;
+    t.tiles_n = (n + HGEMM_BN - 1) / HGEMM_BN;
+    t.alpha = alpha;
+    t.beta = beta;
+    const uint64_t wg = gemm_half_workgroups(m, n, batch);
+    if (wg > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
+    info.kind = LG_PLAN_TILED;
+    info.workgroups = wg;
+}
 
 // (splits, k_chunk): one split when the output already fills the chip or K is short.
 void split_shape(uint64_t tiles, uint32_t k, uint32_t* splits, uint32_t* chunk) {
@@ -423,7 +508,7 @@ int load_mode(uintptr_t base, uint64_t off, uint64_t sb, uint64_t srow, uint64_t
 }
 
 Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, float alpha,
-                 float beta) {
+                 float beta, bool half) {
     Plan p;
     lg_contract_plan& info = p.info;
     info.batch = mg.batch_n;
@@ -440,6 +525,10 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     }
     const bool reads_inputs = alpha != 0.0f && mg.k_n != 0;
     check_destination_alias(a, b, c, mg.m_n, mg.n_n, mg.k_n, reads_inputs);
+    if (half) {
+        plan_half(a, b, c, mg, alpha, beta, reads_inputs, p);
+        return p;
+    }
     float* cptr = reinterpret_cast<float*>(c.base) + c.offset;
     if (!reads_inputs) {
         info.kind = beta == 0.0f ? LG_PLAN_ZERO : LG_PLAN_SCALE;
@@ -544,36 +633,53 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     return p;
 }
 
-void prepare_views(const View& a, const View& b, const View& c) {
-    validate(a, 4);
-    validate(b, 4);
-    validate(c, 4);
+void prepare_views(const View& a, const View& b, const View& c, bool half) {
+    const uint32_t esz = half ? 2 : 4;
+    validate(a, esz);
+    validate(b, esz);
+    validate(c, esz);
 }
 
 Plan plan_contract(float alpha, const lg_view* a_c, const char* la, const lg_view* b_c,
                    const char* lb, float beta, const lg_view* c_c, const char* lc, View* a,
-                   View* b, View* c) {
+                   View* b, View* c, bool half = false) {
     *a = view_from_c(a_c, "A");
     *b = view_from_c(b_c, "B");
     *c = view_from_c(c_c, "C");
-    prepare_views(*a, *b, *c);
+    prepare_views(*a, *b, *c, half);
     const std::string sa = parse_labels(la, a->rank(), "A");
     const std::string sb = parse_labels(lb, b->rank(), "B");
     const std::string sc = parse_labels(lc, c->rank(), "C");
     return plan_merged(*a, *b, *c, merge_all(groups_from_labels(*a, sa, *b, sb, *c, sc)), alpha,
-                       beta);
+                       beta, half);
 }
 
 Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, const lg_view* c_c,
-               View* a, View* b, View* c) {
+               View* a, View* b, View* c, bool half = false) {
     *a = view_from_c(a_c, "A");
     *b = view_from_c(b_c, "B");
     *c = view_from_c(c_c, "C");
-    prepare_views(*a, *b, *c);
-    return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta);
+    prepare_views(*a, *b, *c, half);
+    return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta, half);
 }
 
 void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
+    if (p.half) {
+        switch (p.info.kind) {
+            case LG_PLAN_ZERO:
+            case LG_PLAN_SCALE:
+                launch_fill_half(ctx, s, p.hfill);
+                return;
+            case LG_PLAN_GENERAL:
+                launch_general_half(ctx, s, p.hgeneral);
+                return;
+            case LG_PLAN_TILED:
+                launch_gemm_half(ctx, s, p.hgemm);
+                return;
+            default:
+                return;  // empty
+        }
+    }
     switch (p.info.kind) {
         case LG_PLAN_EMPTY:
             return;
@@ -615,7 +721,7 @@ void run(lg_ctx* ctx, void* stream, Plan plan, bool wait) {
 
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
                         float beta, const View& c) {
-    Plan plan = plan_merged(a, b, c, merge_all(groups_from_gemm(a, b, c)), alpha, beta);
+    Plan plan = plan_merged(a, b, c, merge_all(groups_from_gemm(a, b, c)), alpha, beta, false);
     set_device(ctx);
     execute(ctx, s, plan);
 }
@@ -691,6 +797,74 @@ lg_status lg_plan_gemm_f32(float alpha, const lg_view* a, const lg_view* b, floa
         if (out == nullptr) fail_invalid("null output plan");
         View va, vb, vc;
         *out = plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc).info;
+    });
+}
+
+lg_status lg_encode_contract_f16(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                 const char* a_labels, const lg_view* b, const char* b_labels,
+                                 float beta, const lg_view* c, const char* c_labels) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, stream,
+            plan_contract(alpha, a, a_labels, b, b_labels, beta, c, c_labels, &va, &vb, &vc, true), false);
+    });
+}
+
+lg_status lg_contract_f16(lg_ctx* ctx, float alpha, const lg_view* a, const char* a_labels,
+                          const lg_view* b, const char* b_labels, float beta, const lg_view* c,
+                          const char* c_labels) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, nullptr,
+            plan_contract(alpha, a, a_labels, b, b_labels, beta, c, c_labels, &va, &vb, &vc, true), true);
+    });
+}
+
+lg_status lg_encode_gemm_f16(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                             const lg_view* b, float beta, const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, stream, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc, true), false);
+    });
+}
+
+lg_status lg_gemm_f16(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b, float beta,
+                      const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, nullptr, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc, true), true);
+    });
+}
+
+lg_status lg_gemm_nowait_f16(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b,
+                             float beta, const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        View va, vb, vc;
+        run(ctx, nullptr, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc, true), false);
+    });
+}
+
+lg_status lg_plan_contract_f16(float alpha, const lg_view* a, const char* a_labels,
+                               const lg_view* b, const char* b_labels, float beta,
+                               const lg_view* c, const char* c_labels, lg_contract_plan* out) {
+    return guarded([&] {
+        if (out == nullptr) fail_invalid("null output plan");
+        View va, vb, vc;
+        *out = plan_contract(alpha, a, a_labels, b, b_labels, beta, c, c_labels, &va, &vb, &vc, true).info;
+    });
+}
+
+lg_status lg_plan_gemm_f16(float alpha, const lg_view* a, const lg_view* b, float beta,
+                           const lg_view* c, lg_contract_plan* out) {
+    return guarded([&] {
+        if (out == nullptr) fail_invalid("null output plan");
+        View va, vb, vc;
+        *out = plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc, true).info;
     });
 }
 

@@ -150,6 +150,37 @@ struct FillArgs {
     Axes4 c_batch, c_m, c_n;
 };
 
+// f16 contraction (half operands as raw 16-bit patterns): products of halves are exact in
+// f64, sums run in f64 on the f64 matrix cores, and each output rounds once to f16.
+constexpr int HGEMM_BM = 64, HGEMM_BN = 64, HGEMM_BK = 16;
+struct GemmHalfArgs {
+    const uint16_t* a;
+    const uint16_t* b;
+    uint16_t* c;
+    int64_t a_sb, a_sm, a_sk, b_sb, b_sn, b_sk, c_sb, c_sm, c_sn;
+    uint32_t m, n, k, batch, tiles_m, tiles_n;
+    float alpha, beta;
+};
+struct GeneralHalfArgs {
+    const uint16_t* a;
+    const uint16_t* b;
+    uint16_t* c;
+    uint32_t m, n, k, batch;
+    float alpha, beta;
+    Axes4 a_batch, a_m, a_k, b_batch, b_n, b_k, c_batch, c_m, c_n;
+};
+struct FillHalfArgs {
+    uint16_t* c;
+    uint64_t count;
+    uint32_t m, n, batch;
+    float beta;
+    Axes4 c_batch, c_m, c_n;
+};
+void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args);
+void launch_general_half(Context* ctx, hipStream_t s, const GeneralHalfArgs& args);
+void launch_fill_half(Context* ctx, hipStream_t s, const FillHalfArgs& args);
+uint64_t gemm_half_workgroups(uint32_t m, uint32_t n, uint32_t batch);
+
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode);
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args);
 void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args);

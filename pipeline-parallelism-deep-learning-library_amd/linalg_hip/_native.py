@@ -94,6 +94,14 @@ SIGNATURES = {
     "lg_plan_contract_f32": (i32, [F, VP, cp, VP, cp, F, VP, cp,
                                    ctypes.POINTER(lg_contract_plan)]),
     "lg_plan_gemm_f32": (i32, [F, VP, VP, F, VP, ctypes.POINTER(lg_contract_plan)]),
+    "lg_encode_contract_f16": (i32, [vp, vp, F, VP, cp, VP, cp, F, VP, cp]),
+    "lg_contract_f16": (i32, [vp, F, VP, cp, VP, cp, F, VP, cp]),
+    "lg_encode_gemm_f16": (i32, [vp, vp, F, VP, VP, F, VP]),
+    "lg_gemm_f16": (i32, [vp, F, VP, VP, F, VP]),
+    "lg_gemm_nowait_f16": (i32, [vp, F, VP, VP, F, VP]),
+    "lg_plan_contract_f16": (i32, [F, VP, cp, VP, cp, F, VP, cp,
+                                   ctypes.POINTER(lg_contract_plan)]),
+    "lg_plan_gemm_f16": (i32, [F, VP, VP, F, VP, ctypes.POINTER(lg_contract_plan)]),
     "lg_plan_permute": (i32, [u32, i32, VP, VP, ctypes.POINTER(lg_permute_plan)]),
     "lg_debug_launch_count": (u64, [vp]),
     "lg_debug_launch_name": (cp, [vp, u64]),

@@ -23,6 +23,7 @@ DTYPES = {
     "u32": (N.LG_ELEM_U32, 4, np.uint32),
     "i32": (N.LG_ELEM_I32, 4, np.int32),
     "c64": (N.LG_ELEM_C32, 8, np.complex64),  # [f32; 2] (re, im)
+    "f16": (None, 2, np.float16),             # contraction only (not a permutation element)
 }
 
 

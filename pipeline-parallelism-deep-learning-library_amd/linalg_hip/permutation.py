@@ -26,6 +26,8 @@ def permute_view(view: TensorView, perm: Sequence[int]) -> TensorView:
 def _same_dtype(src: TensorView, dst: TensorView) -> int:
     if src.dtype != dst.dtype:
         raise InvalidArgument(f"source {src.dtype} and destination {dst.dtype} differ")
+    if src.elem is None:
+        raise InvalidArgument(f"{src.dtype} is not a permutation element type")
     return src.elem
 
 

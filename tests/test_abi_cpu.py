@@ -347,3 +347,50 @@ def test_contraction_alias_rules():
     assert C.plan_gemm(-1.0, Lv, Uv, 1.0, Cv)["kind"] in ("tiled", "split")
     # alpha = 0 reads nothing, so aliasing an input is fine there (only C's self-overlap counts).
     assert C.plan_gemm(0.0, whole, other, 1.0, whole)["kind"] == "scale"
+
+
+def test_f16_plans_and_validation():
+    def hv(layout, extra=0, base_shift=0):
+        buf = fake((layout.span() + extra) * 2)
+        if base_shift:
+            buf = L.Buffer(None, buf.base + base_shift, buf.nbytes - 16)
+        return L.TensorView(buf, layout.offset, layout.shape, layout.strides, "f16")
+
+    a, b, c = hv(Layout.dense([64, 48])), hv(Layout.dense([48, 32])), hv(Layout.dense([64, 32]))
+    p = C.plan_gemm(1.0, a, b, 0.0, c)
+    assert (p["kind"], p["a_mode"], p["b_mode"], p["splits"]) == ("tiled", "strided", "strided", 1)
+    assert p["workgroups"] == 1
+    assert C.plan_gemm(0.0, a, b, 0.0, c)["kind"] == "zero"
+    assert C.plan_gemm(0.0, a, b, 0.5, c)["kind"] == "scale"
+    # Tall K never splits on the f16 path (one f64 tile per output block).
+    p = C.plan_gemm(1.0, hv(Layout.dense([4, 300000])), hv(Layout.dense([300000, 4])), 0.0,
+                    hv(Layout.dense([4, 4])))
+    assert (p["kind"], p["splits"]) == ("tiled", 1)
+    # Unmergeable groups take the general kernel.
+    p = C.plan_contract(-1.5, (hv(Layout.with_([5, 7, 6, 9], [2, 0, 3, 1], [1] * 4, 3)), "ijkl"),
+                        (hv(Layout.with_([9, 6, 4, 11], [3, 0, 2, 1], [1, 2, 1, 1], 0)), "lkmn"),
+                        -0.5, (hv(Layout.with_([5, 4, 7, 11], [1, 3, 0, 2], [1, 1, 2, 1], 8)), "imjn"))
+    assert p["kind"] == "general"
+    # A 2-byte-aligned base is fine for halves; an odd address is not.
+    assert C.plan_gemm(1.0, hv(Layout.dense([8, 8]), base_shift=2), hv(Layout.dense([8, 8])),
+                       0.0, hv(Layout.dense([8, 8])))["kind"] == "tiled"
+    with pytest.raises(L.InvalidArgument, match="misaligned"):
+        C.plan_gemm(1.0, hv(Layout.dense([8, 8]), base_shift=1), hv(Layout.dense([8, 8])), 0.0,
+                    hv(Layout.dense([8, 8])))
+    # Capacity counts 2-byte elements: a view one element past the buffer is rejected.
+    buf = fake(64 * 2)
+    full = L.TensorView(buf, 0, [buf.nbytes // 2], [1], "f16")
+    over = L.TensorView(buf, 1, [buf.nbytes // 2], [1], "f16")
+    ok = L.TensorView(fake(4096), 0, [buf.nbytes // 2], [1], "f16")
+    assert C.plan_contract(1.0, (full, "k"), (ok, "k"), 0.0, (hv(Layout.dense([])), ""))["kind"] == "tiled"
+    with pytest.raises(L.InvalidArgument):
+        C.plan_contract(1.0, (over, "k"), (ok, "k"), 0.0, (hv(Layout.dense([])), ""))
+    # Mixed element types are refused before anything runs.
+    with pytest.raises(L.InvalidArgument, match="all-f32 or all-f16"):
+        C.plan_gemm(1.0, a, dense([48, 32]), 0.0, c)
+    # The alias rules are the f32 ones: C may not overlap A.
+    shared = fake(64 * 64 * 2)
+    av = L.TensorView(shared, 0, [64, 48], [48, 1], "f16")
+    cv = L.TensorView(shared, 64, [64, 32], [32, 1], "f16")
+    with pytest.raises(L.Overlap):
+        C.plan_gemm(1.0, av, b, 0.0, cv)

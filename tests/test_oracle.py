@@ -323,3 +323,42 @@ def test_north_star_tolerance_formula():
     b = np.array([4.0, -1.0], np.float32)
     assert oracle.north_star_tol(100, a, b) == pytest.approx(1e-5 * 10 * 2.0 * 4.0)
     assert struct.pack("<f", 1.0) == np.float32(1.0).tobytes()
+
+
+# ---- f16: the single-rounding reference ----------------------------------------------------
+def test_f16_round_exact_agrees_with_numpy_on_doubles():
+    from fractions import Fraction
+    g = np.random.Generator(np.random.PCG64(16))
+    vals = list(g.standard_normal(3000) * np.exp2(g.integers(-30, 18, 3000)))
+    # Ties, the overflow threshold, subnormal boundaries.
+    vals += [1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65504.0, 65519.99, 65520.0, 2.0 ** -24,
+             2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -25 + 2.0 ** -40, 2.0 ** -14 - 2.0 ** -25, -0.5]
+    for v in vals:
+        with np.errstate(over="ignore"):
+            want = int(np.float16(v).view(np.uint16))
+        assert oracle.f16_round_exact(Fraction(v)) == want, v
+
+
+def test_f16_scale_known_answer_from_the_reference():
+    # shaders/contraction.metal:730-733: beta = -0.999 times C = 0x0DDC rounds once to 0x8DDB
+    # (rounding the f32 product first gives 0x8DDA).
+    from fractions import Fraction
+    c = np.uint16(0x0DDC).view(np.float16)
+    beta = np.float32(-0.999)
+    exact = Fraction(float(beta)) * Fraction(float(c))
+    assert oracle.f16_round_exact(exact) == 0x8DDB
+    twice = int(np.float16(np.float32(beta) * np.float32(c)).view(np.uint16))
+    assert twice == 0x8DDA  # the double rounding the reference avoids
+
+
+def test_contract_exact_f16_small_closed_forms():
+    a = np.array([[1, 2], [3, 4]], np.float16)
+    b = np.array([[5, 6], [7, 8]], np.float16)
+    got = oracle.contract_exact_f16(1.0, a, b, 0.0, np.zeros((2, 2), np.float16))
+    assert got.view(np.float16).tolist() == [[19, 22], [43, 50]]
+    # 2048 + 1 is a tie in f16 (spacing 2 above 2048): rounds to even 2048; + 3 rounds to 2052.
+    a = np.array([[2048, 1]], np.float16)
+    b = np.array([[1], [1]], np.float16)
+    assert oracle.contract_exact_f16(1.0, a, b, 0.0, np.zeros((1, 1), np.float16)).view(np.float16)[0, 0] == 2048
+    a = np.array([[2048, 3]], np.float16)
+    assert oracle.contract_exact_f16(1.0, a, b, 0.0, np.zeros((1, 1), np.float16)).view(np.float16)[0, 0] == 2052
