@@ -156,9 +156,24 @@ def bench_gemm_f16(ctx, events, pool, L, C, m, n, k, args):
     ms = timed(ctx, events, lambda: C.encode_gemm(ctx, ctx.queue, 1.0, av, bv, 0.0, cv),
                args.steps, args.warmup)
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    return {"name": f"f16 gemm {m}x{n}x{k} (f64 accumulation, one f16 rounding)", "ms": ms,
-            "tflops": tf, "frac_f64_mfma": tf / PEAK_F64_TFLOPS,
-            "plan": {k_: plan[k_] for k_ in ("kind", "workgroups")}}
+    res = {"name": f"f16 gemm {m}x{n}x{k} (f64 accumulation, one f16 rounding)", "ms": ms,
+           "tflops": tf, "frac_f64_mfma": tf / PEAK_F64_TFLOPS,
+           "plan": {k_: plan[k_] for k_ in ("kind", "workgroups")}}
+    if not args.no_cpu:
+        # The f64 reference of tests/contraction_test.rs:200-268 (oracle/oracle.c), one
+        # thread, on 16 output rows: the reference has no CPU f16 contraction of its own.
+        import oracle
+        ah = a.read(np.float16, 0, m * k).astype(np.float32)
+        bh = b.read(np.float16, 0, k * n).astype(np.float32)
+        rows = 16
+        t0 = time.perf_counter()
+        oracle.contract_f64(1.0, ah[: rows * k], (0, [rows, k], [k, 1]), "mk", bh, (0, [k, n], [n, 1]),
+                            "kn", 0.0, np.zeros(rows * n, np.float32), (0, [rows, n], [n, 1]), "mn")
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(2.0 * rows * n * k / dt / 1e12, 6), "unit": "TFLOP/s",
+                               "cores": 1, "kind": "port",
+                               "sample": f"{rows} of {m} output rows, f64 reference loop ({dt:.2f} s)"}
+    return res
 
 
 def bench_train_ops(events, args, timed_fn):
@@ -196,8 +211,41 @@ def bench_train_ops(events, args, timed_fn):
         out[name] = {"ms": ms, "gbs": gbs, "frac": gbs / PEAK_GBS, "bytes": nbytes,
                      "kernel": kernel}
     hb.close()
+    if not args.no_cpu:
+        cpu_train_ops(out, a, b, rows, cols)
     out["_shape"] = [rows, cols]
     return out
+
+
+def cpu_train_ops(out, a, b, rows, cols):
+    """The crates/cpu loops (oracle/oracle.c, one thread) on a [1024, cols] slab of the same
+    data, the same bytes-per-element accounting as the GPU figures."""
+    import oracle
+    r = 1024
+    x = a[: r * cols].reshape(r, cols)
+    t = b[: r * cols].reshape(r, cols)
+    n = r * cols
+    f4, f2 = 4 * n, 2 * n
+    bias = a[:cols].copy()
+    db = np.zeros(cols, np.float32)
+    h = oracle.f32_to_bf16(x)
+    jobs = [
+        ("gelu", lambda: oracle.gelu(x), 2 * f4),
+        ("gelu_backward", lambda: oracle.gelu_backward(x, t), 3 * f4),
+        ("add_bias", lambda: oracle.add_bias(x, bias), 2 * f4),
+        ("bias_grad", lambda: oracle.bias_grad(x, db), f4),
+        ("mse_grad", lambda: oracle.mse_grad(x, t), 3 * f4),
+        ("sgd_step", lambda: oracle.sgd_step(x, t, 1e-3), 4 * f4),
+        ("convert_f32_bf16", lambda: oracle.f32_to_bf16(x), f4 + f2),
+        ("convert_bf16_f32", lambda: oracle.bf16_to_f32(h), f2 + f4),
+    ]
+    for name, fn, nbytes in jobs:
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        out[name]["cpu_baseline"] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
+                                     "cores": 1, "kind": "port",
+                                     "sample": f"[{r}, {cols}] slab, crates/cpu loop ({dt:.2f} s)"}
 
 
 def traffic_from_profile(name):
@@ -379,6 +427,17 @@ def main() -> int:
                                         "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
                                         "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
                            "cpu_baseline": cpu["permute"] if cpu else None}
+    f16 = results.get("f16")
+    if f16:
+        line["contract_f16"] = {
+            "value": round(f16["tflops"], 3), "unit": "TFLOP/s", "workload": f16["name"],
+            "ms_per_step": round(f16["ms"], 4),
+            "roofline": {"bound": "mfma", "achieved": round(f16["tflops"], 3),
+                         "peak": PEAK_F64_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(f16["frac_f64_mfma"], 4),
+                         "kernel": "gemm_f16_f64mfma (v_mfma_f64_16x16x4_f64)",
+                         "profile": "profiles/gemm_f16_f64mfma_4096.md"},
+            "cpu_baseline": f16.get("cpu_baseline")}
     if train:
         shape = train.pop("_shape")
         line["train_ops"] = {
