@@ -306,6 +306,42 @@ lg_core_error lg_backend_convert(lg_ctx* ctx, void* stream, const lg_tensor* x,
                                  const lg_tensor* y);
 
 /* ---------------------------------------------------------------------------------------
+ * Wire format of stage boundaries (crates/core/src/lib.rs:298-412)
+ *
+ * "LNGL", u32 version 1, u32 dtype tag, u32 ndim (at most 8), ndim u32 extents, then the
+ * row-major payload; little-endian. A malformed message, more than 8 extents or an
+ * undecodable tag is LG_CORE_WIRE; an extent above u32::MAX or an overflowing byte count is
+ * LG_CORE_SHAPE. On error nothing is written.
+ * ------------------------------------------------------------------------------------- */
+
+#define LG_WIRE_HEADER_MAX 48 /* WIRE_HEADER_MAX: 16 + 4 * 8 */
+
+/* write_wire_header (crates/core/src/lib.rs:328-335): writes 16 + 4*rank bytes to `out`. */
+lg_core_error lg_wire_write_header(uint32_t dtype, const uint64_t* shape, uint32_t rank,
+                                   uint8_t out[LG_WIRE_HEADER_MAX], uint64_t* len);
+/* parse_wire_header (crates/core/src/lib.rs:361-389): the payload is bytes[*payload_offset..]
+ * and its length has been checked against the shape. */
+lg_core_error lg_wire_parse_header(const uint8_t* bytes, uint64_t len, uint32_t* dtype,
+                                   uint64_t shape[8], uint32_t* rank, uint64_t* payload_offset);
+/* encode_wire (crates/core/src/lib.rs:309-322) into a caller buffer of `out_cap` bytes (too
+ * small: LG_CORE_SHAPE); a payload of the wrong length is LG_CORE_WIRE. */
+lg_core_error lg_wire_encode(uint32_t dtype, const uint64_t* shape, uint32_t rank,
+                             const void* payload, uint64_t payload_len, uint8_t* out,
+                             uint64_t out_cap, uint64_t* written);
+/* send_tensor's download + encode_wire (crates/pipeline/src/lib.rs:71-80) in one device-to-host
+ * copy straight into the wire buffer: after every earlier call on the context stream, returns
+ * when the bytes are final. The tensor must be row-major at offset 0 (else
+ * LG_CORE_UNSUPPORTED_LAYOUT). Host-memory rate; no kernel runs. */
+lg_core_error lg_wire_encode_tensor(lg_ctx* ctx, const lg_tensor* t, uint8_t* out,
+                                    uint64_t out_cap, uint64_t* written);
+/* recv_tensor's decode_wire + upload (crates/pipeline/src/lib.rs:82-98) into an existing tensor
+ * (Backend::upload_into's rules, crates/core/src/lib.rs:127-134): the message's dtype must be
+ * the tensor's (else LG_CORE_DTYPE) and its shape the tensor's (else LG_CORE_SHAPE); one
+ * host-to-device copy; `bytes` may be reused once this returns. */
+lg_core_error lg_wire_decode_into(lg_ctx* ctx, const uint8_t* bytes, uint64_t len,
+                                  const lg_tensor* t);
+
+/* ---------------------------------------------------------------------------------------
  * Plan inspection (host only; no context, no device work). These run the exact
  * validation and planning of the entry points above and report the plan instead of
  * launching it, so the planner is testable without a GPU.

@@ -26,6 +26,7 @@ SOURCES = [
     "backend.cpp",
     "contraction.cpp",
     "permutation.cpp",
+    "wire.cpp",
     "contraction_kernels.hip",
     "contraction_f16_kernels.hip",
     "permutation_kernels.hip",

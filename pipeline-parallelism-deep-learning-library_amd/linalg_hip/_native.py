@@ -20,6 +20,7 @@ LG_ELEM_F32, LG_ELEM_U32, LG_ELEM_I32, LG_ELEM_C32 = range(4)
 CORE_ERRORS = ["Ok", "Shape", "Dtype", "UnsupportedLayout", "UnsupportedDevice", "Alias",
                "Transport", "Wire", "Schedule"]
 LG_DTYPE_F32, LG_DTYPE_F16, LG_DTYPE_BF16 = 1, 2, 3
+LG_WIRE_HEADER_MAX = 48
 PLAN_KINDS = ["empty", "zero", "scale", "tiled", "split", "general"]
 LOAD_MODES = ["k", "mn", "strided"]
 PERMUTE_KINDS = ["empty", "copy", "tile"]
@@ -91,6 +92,13 @@ SIGNATURES = {
     "lg_backend_mse_grad": (i32, [vp, vp, TP, TP, TP, ctypes.POINTER(F)]),
     "lg_backend_sgd_step": (i32, [vp, vp, TP, TP, F]),
     "lg_backend_convert": (i32, [vp, vp, TP, TP]),
+    "lg_wire_write_header": (i32, [u32, ctypes.POINTER(u64), u32, vp, ctypes.POINTER(u64)]),
+    "lg_wire_parse_header": (i32, [vp, u64, ctypes.POINTER(u32), ctypes.POINTER(u64),
+                                   ctypes.POINTER(u32), ctypes.POINTER(u64)]),
+    "lg_wire_encode": (i32, [u32, ctypes.POINTER(u64), u32, vp, u64, vp, u64,
+                             ctypes.POINTER(u64)]),
+    "lg_wire_encode_tensor": (i32, [vp, TP, vp, u64, ctypes.POINTER(u64)]),
+    "lg_wire_decode_into": (i32, [vp, vp, u64, TP]),
     "lg_plan_contract_f32": (i32, [F, VP, cp, VP, cp, F, VP, cp,
                                    ctypes.POINTER(lg_contract_plan)]),
     "lg_plan_gemm_f32": (i32, [F, VP, VP, F, VP, ctypes.POINTER(lg_contract_plan)]),
