@@ -311,7 +311,10 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=50,
+                    help="untimed launches before the timed ones; the MI355X needs tens of ms "
+                         "of sustained MFMA load to reach its steady clock (5 launches of the "
+                         "4096^3 GEMM measure ~7%% below steady state)")
     ap.add_argument("--only", default=None,
                     help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, train, f16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

@@ -27,17 +27,15 @@ namespace gemm_detail {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = GEMM_BM, BN = GEMM_BN;
-constexpr int PMN = BM + 8;  // pitch of a [k][row] stage (floats)
-static_assert(BM == 128 && BN == 128, "the wave layout below assumes 128x128 tiles");
-
-template <int BK>
+// Stage geometry of one operand whose tile spans R rows (M for A, N for B) and BK k.
+template <int BK, int R>
 struct Geo {
-    static constexpr int PK = BK + 4;                           // pitch of a [row][k] stage
-    static constexpr int LOADS = (BM * BK / 4) / GEMM_THREADS;  // 128-bit loads per thread
-    static_assert(LOADS * GEMM_THREADS * 4 == BM * BK, "tile must split evenly over threads");
+    static constexpr int PK = BK + 4;                          // pitch of a [row][k] stage
+    static constexpr int PR = R + 8;                           // pitch of a [k][row] stage
+    static constexpr int LOADS = (R * BK / 4) / GEMM_THREADS;  // 128-bit loads per thread
+    static_assert(LOADS * GEMM_THREADS * 4 == R * BK, "tile must split evenly over threads");
     template <int MODE>
-    static constexpr int stage() { return MODE == LOAD_MN ? BK * PMN : BM * PK; }
+    static constexpr int stage() { return MODE == LOAD_MN ? BK * PR : R * PK; }
 };
 
 // Workgroup -> (plane, tile_m, tile_n). Workgroups are dealt round-robin to the 8 XCDs, so
@@ -66,16 +64,16 @@ __device__ inline void decode_tile(uint32_t bid, uint32_t total, uint32_t tiles_
 // registers. `p` points at (row 0, k 0) of the tile; srow/sk are the operand's strides.
 // FULL (workgroup-uniform: the whole slice is inside the operand) takes branch-free 128-bit
 // loads so every load of the slice is in flight at once; edge slices predicate each element.
-template <int MODE, bool FULL, int BK>
-__device__ inline void load_slice(floatx4 (&r)[Geo<BK>::LOADS], const float* __restrict__ p,
+template <int MODE, bool FULL, int BK, int R, typename G = Geo<BK, R>>
+__device__ inline void load_slice(floatx4 (&r)[G::LOADS], const float* __restrict__ p,
                                   int64_t srow, int64_t sk, uint32_t rows_left, uint32_t k0,
                                   uint32_t klen, int tid) {
 #pragma unroll
-    for (int i = 0; i < Geo<BK>::LOADS; ++i) {
+    for (int i = 0; i < Geo<BK, R>::LOADS; ++i) {
         const int idx = i * GEMM_THREADS + tid;
         if constexpr (MODE == LOAD_MN) {
-            const uint32_t kr = k0 + idx / (BM / 4);
-            const uint32_t row = (idx % (BM / 4)) * 4;
+            const uint32_t kr = k0 + idx / (R / 4);
+            const uint32_t row = (idx % (R / 4)) * 4;
             const float* q = p + static_cast<int64_t>(kr) * sk + row;
             if (FULL || (kr < klen && row + 4 <= rows_left)) {
                 r[i] = *reinterpret_cast<const floatx4*>(q);
@@ -110,57 +108,61 @@ __device__ inline void load_slice(floatx4 (&r)[Geo<BK>::LOADS], const float* __r
 // Writes a loaded K-slice into its LDS stage. With SCALE (operand A) every element is first
 // multiplied by alpha, so each product the MFMAs form is (alpha*a)*b. alpha is finite here
 // (the planner sends non-finite alpha to the general kernel), so zero padding stays zero.
-template <int MODE, int BK, bool SCALE>
-__device__ inline void store_slice(float* __restrict__ st, const floatx4 (&r)[Geo<BK>::LOADS],
+template <int MODE, int BK, int R, bool SCALE, typename G = Geo<BK, R>>
+__device__ inline void store_slice(float* __restrict__ st, const floatx4 (&r)[G::LOADS],
                                    int tid, float alpha) {
 #pragma unroll
-    for (int i = 0; i < Geo<BK>::LOADS; ++i) {
+    for (int i = 0; i < Geo<BK, R>::LOADS; ++i) {
         const int idx = i * GEMM_THREADS + tid;
         floatx4 v = r[i];
         if constexpr (SCALE) v = v * alpha;
         if constexpr (MODE == LOAD_MN) {
-            const int kr = idx / (BM / 4), row = (idx % (BM / 4)) * 4;
-            *reinterpret_cast<floatx4*>(st + kr * PMN + row) = v;
+            const int kr = idx / (R / 4), row = (idx % (R / 4)) * 4;
+            *reinterpret_cast<floatx4*>(st + kr * Geo<BK, R>::PR + row) = v;
         } else {
             const int row = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
-            *reinterpret_cast<floatx4*>(st + row * Geo<BK>::PK + kq) = v;
+            *reinterpret_cast<floatx4*>(st + row * Geo<BK, R>::PK + kq) = v;
         }
     }
 }
 
-// Operand values of the two 32-row blocks `base_row + {0, 32}` for MFMA steps 4g..4g+3.
-template <int MODE, int BK>
-__device__ inline void read_frag(floatx4 (&v)[2], const float* __restrict__ st, int base_row,
+// Operand values of the NB 32-row blocks `base_row + 32*i` for MFMA steps 4g..4g+3.
+template <int MODE, int BK, int R, int NB>
+__device__ inline void read_frag(floatx4 (&v)[NB], const float* __restrict__ st, int base_row,
                                  int g, int lr, int h) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NB; ++i) {
         const int row = base_row + i * 32 + lr;
         if constexpr (MODE == LOAD_MN) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s) v[i][s] = st[(g * 8 + h * 4 + s) * PMN + row];
+            for (int s = 0; s < 4; ++s) v[i][s] = st[(g * 8 + h * 4 + s) * Geo<BK, R>::PR + row];
         } else {
-            v[i] = *reinterpret_cast<const floatx4*>(st + row * Geo<BK>::PK + g * 8 + h * 4);
+            v[i] = *reinterpret_cast<const floatx4*>(st + row * Geo<BK, R>::PK + g * 8 + h * 4);
         }
     }
 }
 
-__device__ inline void mfma_group(floatx16 (&acc)[2][2], const floatx4 (&av)[2],
-                                  const floatx4 (&bv)[2]) {
+template <int TM, int TN>
+__device__ inline void mfma_group(floatx16 (&acc)[TM][TN], const floatx4 (&av)[TM],
+                                  const floatx4 (&bv)[TN]) {
 #pragma unroll
     for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][st], bv[j][st], acc[i][j],
                                                                  0, 0, 0);
 }
 
-template <int AM, int BMD, int BK, bool PIPE>
-__global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
-    using G = Geo<BK>;
-    constexpr int A_ST = G::template stage<AM>();
-    constexpr int B_ST = G::template stage<BMD>();
+// TM x TN blocks of 32x32 per wave, waves in 2x2: the workgroup tile is (64*TM) x (64*TN).
+template <int AM, int BMD, int BK, bool PIPE, int TM = 2, int TN = 2>
+__global__ __launch_bounds__(GEMM_THREADS, (TM * TN > 4 ? 2 : 1)) void gemm_f32_mfma(GemmArgs p) {
+    constexpr int TBM = 64 * TM, TBN = 64 * TN;
+    using GA = Geo<BK, TBM>;
+    using GB = Geo<BK, TBN>;
+    constexpr int A_ST = GA::template stage<AM>();
+    constexpr int B_ST = GB::template stage<BMD>();
     constexpr int GROUPS = BK / 8;
     __shared__ __attribute__((aligned(16))) float smem[2 * (A_ST + B_ST)];
     float* As = smem;
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
     uint32_t plane, tm, tn;
     decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
     const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t m0 = tm * TBM, n0 = tn * TBN;
     const uint32_t kb = split * p.k_chunk;
     const uint32_t klen = min(p.k - kb, p.k_chunk);
     const uint32_t mrem = p.m - m0, nrem = p.n - n0;
@@ -184,31 +186,31 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
     const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
                      static_cast<int64_t>(kb) * p.b_sk;
 
-    floatx16 acc[2][2];
+    floatx16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    floatx4 ra[G::LOADS], rb[G::LOADS];
+    floatx4 ra[GA::LOADS], rb[GB::LOADS];
     const uint32_t ktiles = (klen + BK - 1) / BK;
     // Workgroup-uniform: the tile's M x N window lies inside the operands, so a K-slice is
     // "full" whenever its k range is.
-    const bool inner = mrem >= BM && nrem >= BN;
+    const bool inner = mrem >= TBM && nrem >= TBN;
     auto load = [&](uint32_t k0) {
         if (inner && k0 + BK <= klen) {
-            load_slice<AM, true, BK>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
-            load_slice<BMD, true, BK>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
+            load_slice<AM, true, BK, TBM>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
+            load_slice<BMD, true, BK, TBN>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
         } else {
-            load_slice<AM, false, BK>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
-            load_slice<BMD, false, BK>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
+            load_slice<AM, false, BK, TBM>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
+            load_slice<BMD, false, BK, TBN>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
         }
     };
     load(0);
-    store_slice<AM, BK, true>(As, ra, tid, p.alpha);
-    store_slice<BMD, BK, false>(Bs, rb, tid, 1.0f);
+    store_slice<AM, BK, TBM, true>(As, ra, tid, p.alpha);
+    store_slice<BMD, BK, TBN, false>(Bs, rb, tid, 1.0f);
     __syncthreads();
 
     for (uint32_t kt = 0; kt < ktiles; ++kt) {
@@ -218,29 +220,29 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
         const float* as = As + s * A_ST;
         const float* bs = Bs + s * B_ST;
         if constexpr (PIPE) {
-            floatx4 fa[2][2], fb[2][2];
-            read_frag<AM, BK>(fa[0], as, wm * 64, 0, lr, h);
-            read_frag<BMD, BK>(fb[0], bs, wn * 64, 0, lr, h);
+            floatx4 fa[2][TM], fb[2][TN];
+            read_frag<AM, BK, TBM, TM>(fa[0], as, wm * 32 * TM, 0, lr, h);
+            read_frag<BMD, BK, TBN, TN>(fb[0], bs, wn * 32 * TN, 0, lr, h);
 #pragma unroll
             for (int g = 0; g < GROUPS; ++g) {
                 if (g + 1 < GROUPS) {
-                    read_frag<AM, BK>(fa[(g + 1) & 1], as, wm * 64, g + 1, lr, h);
-                    read_frag<BMD, BK>(fb[(g + 1) & 1], bs, wn * 64, g + 1, lr, h);
+                    read_frag<AM, BK, TBM, TM>(fa[(g + 1) & 1], as, wm * 32 * TM, g + 1, lr, h);
+                    read_frag<BMD, BK, TBN, TN>(fb[(g + 1) & 1], bs, wn * 32 * TN, g + 1, lr, h);
                 }
-                mfma_group(acc, fa[g & 1], fb[g & 1]);
+                mfma_group<TM, TN>(acc, fa[g & 1], fb[g & 1]);
             }
         } else {
 #pragma unroll
             for (int g = 0; g < GROUPS; ++g) {
-                floatx4 av[2], bv[2];
-                read_frag<AM, BK>(av, as, wm * 64, g, lr, h);
-                read_frag<BMD, BK>(bv, bs, wn * 64, g, lr, h);
-                mfma_group(acc, av, bv);
+                floatx4 av[TM], bv[TN];
+                read_frag<AM, BK, TBM, TM>(av, as, wm * 32 * TM, g, lr, h);
+                read_frag<BMD, BK, TBN, TN>(bv, bs, wn * 32 * TN, g, lr, h);
+                mfma_group<TM, TN>(acc, av, bv);
             }
         }
         if (more) {
-            store_slice<AM, BK, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
-            store_slice<BMD, BK, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);
+            store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
+            store_slice<BMD, BK, TBN, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);
         }
         __syncthreads();
     }
@@ -250,13 +252,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
     if (p.partial != nullptr) {
         float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                    const uint32_t col = n0 + wn * 64 + j * 32 + lr;
+                    const uint32_t row = m0 + wm * 32 * TM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                    const uint32_t col = n0 + wn * 32 * TN + j * 32 + lr;
                     if (inner || (row < p.m && col < p.n)) {
                         P[static_cast<int64_t>(row) * p.n + col] = acc[i][j][r];
                     }
@@ -265,13 +267,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_mfma(GemmArgs p) {
     }
     float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                const uint32_t col = n0 + wn * 64 + j * 32 + lr;
+                const uint32_t row = m0 + wm * 32 * TM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                const uint32_t col = n0 + wn * 32 * TN + j * 32 + lr;
                 if (inner || (row < p.m && col < p.n)) {
                     float* q = C + static_cast<int64_t>(row) * p.c_sm +
                                static_cast<int64_t>(col) * p.c_sn;
