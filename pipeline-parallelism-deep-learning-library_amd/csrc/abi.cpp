@@ -201,6 +201,11 @@ void lg_ctx_destroy(lg_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->mse_scratch != nullptr) (void)hipFree(ctx->mse_scratch);
     if (ctx->mse_host != nullptr) (void)hipHostFree(ctx->mse_host);
+    if (ctx->split_stream != nullptr && ctx->split_stream != ctx->stream) {
+        (void)hipEventSynchronize(ctx->split_event);  // the last use was on a caller's stream
+    }
+    if (ctx->split_scratch != nullptr) (void)hipFree(ctx->split_scratch);
+    if (ctx->split_event != nullptr) (void)hipEventDestroy(ctx->split_event);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }

@@ -23,8 +23,11 @@ namespace lg {
 namespace {
 
 constexpr uint64_t EXACT_LIMIT = 2000000;  // src/ops/contraction.rs:584
+#ifndef LG_SPLIT_MIN_CHUNK
+#define LG_SPLIT_MIN_CHUNK 128
+#endif
 constexpr uint32_t SPLIT_TARGET = 512;     // workgroups the split-K path aims for
-constexpr uint32_t SPLIT_MIN_CHUNK = 256;  // K elements per split, at least
+constexpr uint32_t SPLIT_MIN_CHUNK = LG_SPLIT_MIN_CHUNK;  // K elements per split, at least
 constexpr uint32_t SPLIT_MAX = 1024;
 
 struct Axis {
@@ -474,6 +477,8 @@ void plan_half(const View& a, const View& b, const View& c, const Merged& mg, fl
     t.batch = batch;
     t.tiles_m = (m + HGEMM_BM - 1) / HGEMM_BM;
     t.tiles_n = (n + HGEMM_BN - 1) / HGEMM_BN;
+    info.tile_m = HGEMM_BM;
+    info.tile_n = HGEMM_BN;
     t.alpha = alpha;
     t.beta = beta;
     const uint64_t wg = gemm_half_workgroups(m, n, batch);
@@ -599,8 +604,17 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     t.batch = batch;
     t.alpha = alpha;
     t.beta = beta;
-    t.tiles_m = (m + GEMM_BM - 1) / GEMM_BM;
-    t.tiles_n = (n + GEMM_BN - 1) / GEMM_BN;
+    // 128x128 tiles load half the operand bytes per product of 64x64 ones, so they are kept
+    // whenever their grid, split along K as far as split_shape would go, reaches
+    // GEMM_SMALL_BELOW workgroups; otherwise 64x64 tiles give four times the workgroups
+    // before split-K adds more.
+    const uint64_t big = static_cast<uint64_t>((m + GEMM_BM - 1) / GEMM_BM) *
+                         ((n + GEMM_BN - 1) / GEMM_BN) * batch;
+    const uint64_t k_ways = std::max<uint64_t>(1, std::min<uint64_t>(k / SPLIT_MIN_CHUNK, SPLIT_MAX));
+    t.tile = big * k_ways < GEMM_SMALL_BELOW ? GEMM_SMALL_TILE : GEMM_BM;
+    t.tiles_m = (m + t.tile - 1) / t.tile;
+    t.tiles_n = (n + t.tile - 1) / t.tile;
+    info.tile_m = info.tile_n = t.tile;
     const int a_mode = load_mode(a.base, a.offset, ab.a, am.a, ak.a);
     const int b_mode = load_mode(b.base, b.offset, ab.b, an.b, ak.b);
     info.a_mode = static_cast<uint32_t>(a_mode);
@@ -613,7 +627,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     t.k_chunk = chunk;
     info.splits = splits;
     info.k_chunk = chunk;
-    info.workgroups = gemm_workgroups(m, n, batch, splits);
+    info.workgroups = gemm_workgroups(m, n, batch, splits, t.tile);
     if (splits == 1) {
         info.kind = LG_PLAN_TILED;
         return p;
@@ -663,6 +677,40 @@ Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, 
     return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta, half);
 }
 
+// The context's split-K buffer, at least `bytes` long, ordered after every earlier use.
+// Called with ctx->split_lock held.
+float* split_scratch(lg_ctx* ctx, hipStream_t s, uint64_t bytes) {
+    if (ctx->split_event == nullptr) {
+        check_hip(hipEventCreateWithFlags(&ctx->split_event, hipEventDisableTiming),
+                  "hipEventCreateWithFlags");
+    }
+    // Back-to-back calls on the context's own stream are ordered by it. Any other pair waits
+    // on the event, also when both are one caller's stream handle: the handle may name a new
+    // stream created after the old one was destroyed with work still queued.
+    const bool own = s == ctx->stream && ctx->split_stream == ctx->stream;
+    if (ctx->split_stream != nullptr && !own) {
+        if (ctx->split_stream == ctx->stream) {
+            check_hip(hipEventRecord(ctx->split_event, ctx->stream), "hipEventRecord");
+        }
+        check_hip(hipStreamWaitEvent(s, ctx->split_event, 0), "hipStreamWaitEvent");
+    }
+    if (bytes > ctx->split_bytes) {
+        if (ctx->split_scratch != nullptr) {
+            // `s` is now ordered after every use of the old buffer; let them finish first.
+            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+            check_hip(hipFree(ctx->split_scratch), "hipFree");
+            ctx->split_scratch = nullptr;
+            ctx->split_bytes = 0;
+        }
+        void* p = nullptr;
+        check_hip(hipMalloc(&p, bytes), "hipMalloc");
+        ctx->split_scratch = p;
+        ctx->split_bytes = bytes;
+    }
+    ctx->split_stream = s;
+    return static_cast<float*>(ctx->split_scratch);
+}
+
 void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
     if (p.half) {
         switch (p.info.kind) {
@@ -695,16 +743,18 @@ void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
                         static_cast<int>(p.info.b_mode));
             return;
         case LG_PLAN_SPLIT: {
-            // Stream-ordered scratch: freed after the reduction on the same stream, so it
-            // outlives the enqueued work without host-side tracking.
-            void* partial = nullptr;
-            check_hip(hipMallocAsync(&partial, p.info.scratch_bytes, s), "hipMallocAsync");
-            p.gemm.partial = static_cast<float*>(partial);
-            p.reduce.partial = static_cast<const float*>(partial);
+            std::lock_guard<std::mutex> hold(ctx->split_lock);
+            float* partial = split_scratch(ctx, s, p.info.scratch_bytes);
+            p.gemm.partial = partial;
+            p.reduce.partial = partial;
             launch_gemm(ctx, s, p.gemm, static_cast<int>(p.info.a_mode),
                         static_cast<int>(p.info.b_mode));
             launch_reduce(ctx, s, p.reduce);
-            check_hip(hipFreeAsync(partial, s), "hipFreeAsync");
+            if (s != ctx->stream) {
+                // Marks the end of this use for a later call on another stream; the context's
+                // own stream outlives the buffer, so its uses are marked only when needed.
+                check_hip(hipEventRecord(ctx->split_event, s), "hipEventRecord");
+            }
             return;
         }
     }

@@ -149,20 +149,25 @@ void check_launch(const char* what) { check_hip(hipGetLastError(), what); }
 
 template <int AM, int BMD>
 void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
-    hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, GEMM_PIPE>), dim3(groups),
-                       dim3(GEMM_THREADS), 0, s, a);
+    if (a.tile == GEMM_SMALL_TILE) {
+        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, GEMM_PIPE, 1, 1>), dim3(groups),
+                           dim3(GEMM_THREADS), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, GEMM_PIPE, 2, 2>), dim3(groups),
+                           dim3(GEMM_THREADS), 0, s, a);
+    }
 }
 
 }  // namespace
 
-uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits) {
-    const uint64_t tm = (m + GEMM_BM - 1) / GEMM_BM, tn = (n + GEMM_BN - 1) / GEMM_BN;
+uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits, uint32_t tile) {
+    const uint64_t tm = (m + tile - 1) / tile, tn = (n + tile - 1) / tile;
     return tm * tn * batch * splits;
 }
 
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode) {
     const uint32_t groups =
-        static_cast<uint32_t>(gemm_workgroups(args.m, args.n, args.batch, args.splits));
+        static_cast<uint32_t>(gemm_workgroups(args.m, args.n, args.batch, args.splits, args.tile));
     static const char* const names[3][3] = {
         {"gemm_f32_mfma<K,K>", "gemm_f32_mfma<K,MN>", "gemm_f32_mfma<K,S>"},
         {"gemm_f32_mfma<MN,K>", "gemm_f32_mfma<MN,MN>", "gemm_f32_mfma<MN,S>"},

@@ -72,6 +72,16 @@ struct Context {
     std::mutex mse_lock;
     void* mse_scratch = nullptr;
     float* mse_host = nullptr;
+    // Split-K partials: one grow-only buffer per context, reused call after call (a
+    // stream-ordered malloc/free per call costs tens of microseconds of host time). split_lock
+    // is held while a call hands the buffer to its two launches. Calls on one stream are
+    // ordered by the stream; a call on another stream first waits for split_event, which
+    // marks the end of the previous user's work.
+    std::mutex split_lock;
+    void* split_scratch = nullptr;
+    uint64_t split_bytes = 0;
+    hipStream_t split_stream = nullptr;  // stream of the last call that used the buffer
+    hipEvent_t split_event = nullptr;
 };
 void note_launch(Context* ctx, const char* name);
 void set_last_error(const std::string& msg);
@@ -98,9 +108,15 @@ lg_status guarded(F&& body) {
 // ---------------------------------------------------------------------------------------
 enum LoadMode : int { LOAD_K = 0, LOAD_MN = 1, LOAD_S = 2 };
 
-// Tile geometry of the MFMA GEMM kernel.
+// Tile geometry of the MFMA GEMM kernel: 128x128 output tiles, or 64x64 (GEMM_SMALL_TILE)
+// when the 128x128 grid, even split along K, has fewer than GEMM_SMALL_BELOW workgroups.
 constexpr uint32_t GEMM_BM = 128;
 constexpr uint32_t GEMM_BN = 128;
+#ifndef LG_GEMM_SMALL_BELOW
+#define LG_GEMM_SMALL_BELOW 256
+#endif
+constexpr uint32_t GEMM_SMALL_TILE = 64;
+constexpr uint64_t GEMM_SMALL_BELOW = LG_GEMM_SMALL_BELOW;
 constexpr uint32_t GEMM_BK = 16;       // K-slice depth per LDS stage
 constexpr bool GEMM_PIPE = true;       // double-buffer LDS fragments across MFMA groups
 constexpr uint32_t GEMM_THREADS = 256;
@@ -117,6 +133,7 @@ struct GemmArgs {
     uint32_t k_chunk, splits;
     uint32_t tiles_m, tiles_n;
     float alpha, beta;
+    uint32_t tile;  // output tile edge: GEMM_BM (128) or GEMM_SMALL_TILE (64)
 };
 
 struct ReduceArgs {
@@ -185,7 +202,7 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args);
 void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args);
 void launch_fill(Context* ctx, hipStream_t s, const FillArgs& args);
-uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits);
+uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits, uint32_t tile);
 
 // ---------------------------------------------------------------------------------------
 // Permutation kernels

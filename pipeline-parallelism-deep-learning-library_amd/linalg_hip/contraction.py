@@ -83,7 +83,8 @@ def _plan_dict(p: N.lg_contract_plan) -> dict:
     return {"kind": N.PLAN_KINDS[p.kind], "a_mode": N.LOAD_MODES[p.a_mode],
             "b_mode": N.LOAD_MODES[p.b_mode], "groups": p.groups, "batch": p.batch, "m": p.m,
             "n": p.n, "k": p.k, "splits": p.splits, "k_chunk": p.k_chunk,
-            "workgroups": p.workgroups, "scratch_bytes": p.scratch_bytes}
+            "workgroups": p.workgroups, "scratch_bytes": p.scratch_bytes,
+            "tile": (p.tile_m, p.tile_n)}
 
 
 def plan_contract(alpha: float, a, b, beta: float, c) -> dict:

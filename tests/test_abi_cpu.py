@@ -214,25 +214,44 @@ def dense(shape, **kw):
     return view(Layout.dense(shape), **kw)
 
 
+def test_output_tile_choice():
+    # 17 x 17 = 289 tiles of 128x128: the large tile; 15 x 16 = 240: 64x64 (30 x 31 of them).
+    p = C.plan_gemm(1.0, dense([2100, 37]), dense([37, 2050]), 0.0, dense([2100, 2050]))
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (128, 128), 289)
+    p = C.plan_gemm(1.0, dense([1900, 45]), dense([45, 1950]), 0.0, dense([1900, 1950]))
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (64, 64), 30 * 31)
+    # Small output, long K: 64x64 tiles, then split-K up to the workgroup target.
+    p = C.plan_gemm(1.0, dense([200, 2000]), dense([2000, 190]), 0.0, dense([200, 190]))
+    assert (p["kind"], p["tile"]) == ("split", (64, 64))
+    assert p["workgroups"] == 4 * 3 * p["splits"] and p["splits"] > 1
+    # The f16 path has one 64x64 tile kernel.
+    h = lambda s: view(Layout.dense(s), dtype="f16")
+    assert C.plan_gemm(1.0, h([300, 40]), h([40, 300]), 0.0, h([300, 300]))["tile"] == (64, 64)
+
+
 def test_contraction_plans_for_the_baseline_configs():
     p = C.plan_gemm(1.0, dense([512, 512]), dense([512, 512]), 0.0, dense([512, 512]))
     assert p["kind"] in ("tiled", "split") and p["a_mode"] == "k" and p["b_mode"] == "mn"
+    assert p["tile"] == (64, 64)  # 16 tiles of 128x128 would leave most of the chip idle
     # Config 3: B given as a permuted view "bkj" of [32, j, k] storage (unit stride along k).
     bstore = dense([32, 1024, 1024])
     bview = P.permute_view(bstore, [0, 2, 1])
     p = C.plan_contract(1.0, (dense([32, 1024, 1024]), "bik"), (bview, "bkj"), 0.0,
                         (dense([32, 1024, 1024]), "bij"))
     assert p["kind"] == "tiled" and p["batch"] == 32 and p["b_mode"] == "k" and p["a_mode"] == "k"
+    assert p["tile"] == (128, 128)
     # Config 4: tall K goes split-K with a fixed chunk grid.
     p = C.plan_gemm(1.0, dense([256, 65536]), dense([65536, 256]), 0.0, dense([256, 256]))
     assert p["kind"] == "split" and p["splits"] > 1 and p["k_chunk"] % 32 == 0
+    assert p["tile"] == (128, 128)  # split-K alone fills the chip: keep the large tile
     assert p["splits"] * p["k_chunk"] >= 65536 > (p["splits"] - 1) * p["k_chunk"]
     assert p["scratch_bytes"] == p["splits"] * 256 * 256 * 4
     # Config 5: transpose_matrix views (strides [1, rows]) are read in place.
     X, W, dY = dense([4096, 4096]), dense([4096, 16384]), dense([4096, 16384])
     Wt = L.TensorView(W.buffer, 0, [16384, 4096], [1, 16384])
     Xt = L.TensorView(X.buffer, 0, [4096, 4096], [1, 4096])
-    assert C.plan_gemm(1.0, X, W, 0.0, dense([4096, 16384]))["kind"] == "tiled"
+    p = C.plan_gemm(1.0, X, W, 0.0, dense([4096, 16384]))
+    assert p["kind"] == "tiled" and p["tile"] == (128, 128) and p["workgroups"] == 32 * 128
     p = C.plan_gemm(1.0, dY, Wt, 0.0, dense([4096, 4096]))
     assert (p["a_mode"], p["b_mode"]) == ("k", "k")
     p = C.plan_gemm(1.0, Xt, dY, 1.0, dense([4096, 16384]))

@@ -336,6 +336,50 @@ def test_shared_stream_orders_dependent_work(ctx, pool):
                                                  "ij"), "Gram")
 
 
+def test_split_partials_shared_across_streams():
+    """A context's split-K partial buffer serves calls on its own stream and on two caller
+    streams, enqueued back to back with no host wait and growing three times on the way;
+    every result matches the oracle. The context is then destroyed after a last use on a
+    caller stream."""
+    import linalg_hip as L
+    from helpers import Pool
+    ctx2 = L.Context.new(0)
+    p2 = Pool(ctx2)
+    s1, s2 = ctx2.new_stream(), ctx2.new_stream()
+    try:
+        shapes = [(8, 8, 65536), (40, 24, 30000), (130, 200, 20000), (192, 128, 40000),
+                  (3, 5, 200001)]
+        streams = [s1, ctx2.queue, s2, s1, ctx2.queue]
+        jobs, last = [], 0
+        for i, (m, n, k) in enumerate(shapes):
+            g = rng(2100 + i)
+            a = Tensor.random(p2, Layout.dense([m, k]), g)
+            b = Tensor.random(p2, Layout.dense([k, n]), g)
+            c = Tensor(p2, Layout.dense([m, n]))
+            plan = C.plan_gemm(1.0, a.view(), b.view(), 0.0, c.view())
+            assert plan["kind"] == "split", (m, n, k, plan)
+            jobs.append((a, b, c, plan["scratch_bytes"] > last))
+            last = max(last, plan["scratch_bytes"])
+        assert sum(grow for *_, grow in jobs) >= 4  # the first call allocates, three grow it
+        for (a, b, c, _), s in zip(jobs, streams):
+            C.encode_gemm(ctx2, s, 1.0, a.view(), b.view(), 0.0, c.view())
+        s1.wait_until_completed()
+        s2.wait_until_completed()
+        ctx2.sync()
+        for (a, b, c, _), (m, n, k) in zip(jobs, shapes):
+            want = oracle.contract_f64(1.0, a.host, a.layout.tup(), "mk", b.host, b.layout.tup(),
+                                       "kn", 0.0, c.host, c.layout.tup(), "mn")
+            oracle.gate(c.read(), want, f"gemm {m}x{n}x{k} across streams")
+        a, b, c, _ = jobs[0]
+        C.encode_gemm(ctx2, s2, 1.0, a.view(), b.view(), 0.0, c.view())
+        s2.wait_until_completed()
+    finally:
+        s1.close()
+        s2.close()
+        p2.free_all()
+        ctx2.close()
+
+
 # --------------------------------------------------------------------------------------
 # Random einsum sweep (tests/contraction_test.rs:1008-1096), own seeded generator.
 # --------------------------------------------------------------------------------------
@@ -393,6 +437,17 @@ def test_tile_edge_sweep(ctx, pool):
                 alpha, beta = [(1.0, 0.0), (-0.75, 1.0), (0.5, -0.5), (2.0, 0.0)][seed % 4]
                 Case.matmul(m, n, k).scalars(alpha, beta).run(ctx, pool, seed)
                 seed += 1
+
+
+def test_both_output_tiles_on_ragged_edges(ctx, pool):
+    """Grids of at least 256 128x128 tiles take 128x128 tiles, smaller ones with short K
+    64x64 (with split-K on top when K allows): ragged M/N/K at each, against both oracles."""
+    seed = 6100
+    for m, n, k in [(2100, 2050, 37), (2047, 2177, 129), (1900, 1950, 45), (130, 250, 300),
+                    (200, 190, 2000)]:
+        alpha, beta = [(1.0, 0.0), (-0.75, 1.0), (0.5, -0.5)][seed % 3]
+        Case.matmul(m, n, k).scalars(alpha, beta).run(ctx, pool, seed)
+        seed += 1
 
 
 # --------------------------------------------------------------------------------------
