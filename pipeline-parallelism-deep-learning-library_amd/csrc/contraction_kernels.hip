@@ -150,10 +150,10 @@ void check_launch(const char* what) { check_hip(hipGetLastError(), what); }
 template <int AM, int BMD>
 void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
     if (a.tile == GEMM_SMALL_TILE) {
-        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, GEMM_PIPE, 1, 1>), dim3(groups),
+        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 1, 1>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);
     } else {
-        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, GEMM_PIPE, 2, 2>), dim3(groups),
+        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 2, 2>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);
     }
 }

@@ -1,9 +1,9 @@
 // The fp32 MFMA GEMM kernel of the contraction path, parameterized by pipeline shape.
 //
-// gemm_f32_mfma<AM, BMD, BK, PIPE>: C = beta * C + sum_k (alpha * a) * b (or raw split-K
-// partials of the sum) for
-// one stride per group. 128x128 output tile per 256-thread workgroup (4 waves in 2x2, each
-// wave 64x64 = 2x2 blocks of v_mfma_f32_32x32x2_f32 accumulating in fp32). K advances BK at a
+// gemm_f32_mfma<AM, BMD, BK, TM, TN>: C = beta * C + sum_k (alpha * a) * b (or raw split-K
+// partials of the sum) for one stride per group. A (64*TM) x (64*TN) output tile per
+// 256-thread workgroup (4 waves in 2x2, each wave TM x TN blocks of v_mfma_f32_32x32x2_f32
+// accumulating in fp32); the product uses 128x128 and, for small grids, 64x64. K advances BK at a
 // time through two LDS stages: while the MFMAs consume stage s, the next K-slice is already in
 // flight from HBM into registers, and is written to stage s^1 before the one barrier per
 // slice. Operand loads follow the operand's unit-stride axis so a transposed or permuted
@@ -13,8 +13,13 @@
 //   LOAD_S  : anything else         -> 32-bit predicated loads into the [row][k] layout
 // Inside a K-slice, MFMA step s of lane half h uses k = 8*(s/4) + 4*h + s%4, so a [row][k]
 // stage hands each lane four consecutive k with one ds_read_b128. A and B agree on this order,
-// so every product pairs the same k. With PIPE, the LDS fragments of step group g+1 are read
-// while the 16 MFMAs of group g run (register double buffer), hiding LDS latency.
+// so every product pairs the same k.
+// The 128x128 kernel is held to 128 VGPRs (accumulators included) so four workgroups share a
+// compute unit: one wave per SIMD from each, whose LDS waits and barriers the other three
+// cover. With that much cover, reading each step group's fragments just before its MFMAs
+// beats double-buffering them in registers, and the MFMA block runs at raised wave priority
+// so a wave that has its operands issues ahead of waves busy with loads. The strided (LOAD_S)
+// forms need more registers than that and keep the compiler's default.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -156,8 +161,10 @@ __device__ inline void mfma_group(floatx16 (&acc)[TM][TN], const floatx4 (&av)[T
 }
 
 // TM x TN blocks of 32x32 per wave, waves in 2x2: the workgroup tile is (64*TM) x (64*TN).
-template <int AM, int BMD, int BK, bool PIPE, int TM = 2, int TN = 2>
-__global__ __launch_bounds__(GEMM_THREADS, (TM * TN > 4 ? 2 : 1)) void gemm_f32_mfma(GemmArgs p) {
+template <int AM, int BMD, int BK, int TM, int TN>
+__global__ __launch_bounds__(GEMM_THREADS, (AM == LOAD_S || BMD == LOAD_S) ? 1 : 4)
+void gemm_f32_mfma(GemmArgs p) {
+    static_assert(TM * TN <= 4, "the occupancy bound assumes at most 2x2 blocks per wave");
     constexpr int TBM = 64 * TM, TBN = 64 * TN;
     using GA = Geo<BK, TBM>;
     using GB = Geo<BK, TBN>;
@@ -219,27 +226,15 @@ __global__ __launch_bounds__(GEMM_THREADS, (TM * TN > 4 ? 2 : 1)) void gemm_f32_
         if (more) load((kt + 1) * BK);
         const float* as = As + s * A_ST;
         const float* bs = Bs + s * B_ST;
-        if constexpr (PIPE) {
-            floatx4 fa[2][TM], fb[2][TN];
-            read_frag<AM, BK, TBM, TM>(fa[0], as, wm * 32 * TM, 0, lr, h);
-            read_frag<BMD, BK, TBN, TN>(fb[0], bs, wn * 32 * TN, 0, lr, h);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int g = 0; g < GROUPS; ++g) {
-                if (g + 1 < GROUPS) {
-                    read_frag<AM, BK, TBM, TM>(fa[(g + 1) & 1], as, wm * 32 * TM, g + 1, lr, h);
-                    read_frag<BMD, BK, TBN, TN>(fb[(g + 1) & 1], bs, wn * 32 * TN, g + 1, lr, h);
-                }
-                mfma_group<TM, TN>(acc, fa[g & 1], fb[g & 1]);
-            }
-        } else {
-#pragma unroll
-            for (int g = 0; g < GROUPS; ++g) {
-                floatx4 av[TM], bv[TN];
-                read_frag<AM, BK, TBM, TM>(av, as, wm * 32 * TM, g, lr, h);
-                read_frag<BMD, BK, TBN, TN>(bv, bs, wn * 32 * TN, g, lr, h);
-                mfma_group<TM, TN>(acc, av, bv);
-            }
+        for (int g = 0; g < GROUPS; ++g) {
+            floatx4 av[TM], bv[TN];
+            read_frag<AM, BK, TBM, TM>(av, as, wm * 32 * TM, g, lr, h);
+            read_frag<BMD, BK, TBN, TN>(bv, bs, wn * 32 * TN, g, lr, h);
+            mfma_group<TM, TN>(acc, av, bv);
         }
+        __builtin_amdgcn_s_setprio(0);
         if (more) {
             store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
             store_slice<BMD, BK, TBN, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);

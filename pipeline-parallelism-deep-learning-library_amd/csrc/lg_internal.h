@@ -118,7 +118,6 @@ constexpr uint32_t GEMM_BN = 128;
 constexpr uint32_t GEMM_SMALL_TILE = 64;
 constexpr uint64_t GEMM_SMALL_BELOW = LG_GEMM_SMALL_BELOW;
 constexpr uint32_t GEMM_BK = 16;       // K-slice depth per LDS stage
-constexpr bool GEMM_PIPE = true;       // double-buffer LDS fragments across MFMA groups
 constexpr uint32_t GEMM_THREADS = 256;
 
 struct GemmArgs {
