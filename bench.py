@@ -470,7 +470,7 @@ def main() -> int:
             "roofline": {"bound": "mfma", "achieved": round(f16["tflops"], 3),
                          "peak": PEAK_F64_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(f16["frac_f64_mfma"], 4),
-                         "kernel": "gemm_f16_f64mfma (v_mfma_f64_16x16x4_f64)",
+                         "kernel": "gemm_f16_f64mfma<0, 1> (v_mfma_f64_16x16x4_f64)",
                          "profile": "profiles/gemm_f16_f64mfma_4096.md"},
             "cpu_baseline": f16.get("cpu_baseline")}
     if train:

@@ -404,6 +404,16 @@ struct Plan {
     FillHalfArgs hfill{};
 };
 
+// 64-bit loads of four halves need the view's first element 8-byte aligned and every other
+// stride a multiple of four elements.
+int load_mode_half(uintptr_t base, uint64_t off, uint64_t sb, uint64_t srow, uint64_t sk) {
+    auto al = [](uint64_t x) { return x % 4 == 0; };
+    const bool start = (base + off * 2) % 8 == 0;
+    if (sk == 1 && start && al(srow) && al(sb)) return LOAD_K;
+    if (srow == 1 && start && al(sk) && al(sb)) return LOAD_MN;
+    return LOAD_S;
+}
+
 // The f16 plans: the same kinds, on the f16 kernels. No split-K: one f64 tile per output block.
 void plan_half(const View& a, const View& b, const View& c, const Merged& mg, float alpha,
                float beta, bool reads_inputs, Plan& p) {
@@ -479,6 +489,8 @@ void plan_half(const View& a, const View& b, const View& c, const Merged& mg, fl
     t.tiles_n = (n + HGEMM_BN - 1) / HGEMM_BN;
     info.tile_m = HGEMM_BM;
     info.tile_n = HGEMM_BN;
+    info.a_mode = static_cast<uint32_t>(load_mode_half(a.base, a.offset, ab.a, am.a, ak.a));
+    info.b_mode = static_cast<uint32_t>(load_mode_half(b.base, b.offset, ab.b, an.b, ak.b));
     t.alpha = alpha;
     t.beta = beta;
     const uint64_t wg = gemm_half_workgroups(m, n, batch);
@@ -722,7 +734,8 @@ void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
                 launch_general_half(ctx, s, p.hgeneral);
                 return;
             case LG_PLAN_TILED:
-                launch_gemm_half(ctx, s, p.hgemm);
+                launch_gemm_half(ctx, s, p.hgemm, static_cast<int>(p.info.a_mode),
+                                 static_cast<int>(p.info.b_mode));
                 return;
             default:
                 return;  // empty

@@ -68,25 +68,85 @@ __device__ inline uint16_t finish(double acc, float alpha, float beta, const uin
 // v_mfma_f64_16x16x4_f64. Block operand layout (checked on gfx950): A lane l holds row l%16,
 // k l/16; B lane l holds column l%16, k l/16; accumulator value v of lane l is row 4*v + l/16,
 // column l%16 (rows interleave across the four 16-lane groups).
-// K advances 16 at a time: the slice is loaded as halves (all 8 loads in flight when the tile
-// and slice lie inside the operands), widened to f64 and staged in LDS.
+// K advances 16 at a time through two LDS stages of f64: while the MFMAs consume stage s, the
+// next slice is in flight from memory into registers (four halves per thread and operand, one
+// 64-bit load when the operand is contiguous along the tile's short axis), and is widened and
+// written to stage s^1 before the one barrier per slice. 34 KB of LDS and under 128 VGPRs
+// keep four workgroups on a compute unit.
 constexpr int HT = 256;
 constexpr int APITCH = HGEMM_BK + 1;  // doubles; odd pitch spreads the k-column reads
 constexpr int BPITCH = HGEMM_BN + 1;
+constexpr int A_STAGE = HGEMM_BM * APITCH;
+constexpr int B_STAGE = HGEMM_BK * BPITCH;
+static_assert(HGEMM_BM * HGEMM_BK == 4 * HT && HGEMM_BN * HGEMM_BK == 4 * HT,
+              "each thread stages four halves of A and four of B per slice");
 
-__global__ __launch_bounds__(HT) void gemm_f16_f64mfma(GemmHalfArgs p) {
-    __shared__ double As[HGEMM_BM * APITCH];
-    __shared__ double Bs[HGEMM_BK * BPITCH];
+typedef uint16_t h4 __attribute__((ext_vector_type(4)));
+
+// Four halves of one operand's K-slice for thread `tid`. `p` is (row 0, k 0) of the tile,
+// srow/sk its strides; the thread's halves run along k (LOAD_K, LOAD_S) or along the row axis
+// (LOAD_MN). FULL: the slice lies inside the operand, so no predicates.
+template <int MODE, bool FULL, int ROWS>
+__device__ inline h4 load4(const uint16_t* __restrict__ p, int64_t srow, int64_t sk,
+                           uint32_t rows_left, uint32_t k0, uint32_t klen, int tid) {
+    h4 r;
+    if constexpr (MODE == LOAD_MN) {
+        const uint32_t kr = k0 + tid / (ROWS / 4), row = (tid % (ROWS / 4)) * 4;
+        const uint16_t* q = p + static_cast<int64_t>(kr) * sk + row;
+        if (FULL) return *reinterpret_cast<const h4*>(q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (kr < klen && row + e < rows_left) ? q[e] : uint16_t(0);
+    } else {
+        const uint32_t row = tid / (HGEMM_BK / 4), kk = k0 + (tid % (HGEMM_BK / 4)) * 4;
+        const uint16_t* q = p + static_cast<int64_t>(row) * srow;
+        if constexpr (MODE == LOAD_K) {
+            if (FULL) return *reinterpret_cast<const h4*>(q + kk);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            r[e] = (FULL || (row < rows_left && kk + e < klen))
+                       ? q[static_cast<int64_t>(kk + e) * sk] : uint16_t(0);
+        }
+    }
+    return r;
+}
+
+// Widens the four halves and writes them to the stage: A as [row][k] (pitch APITCH), B as
+// [k][col] (pitch BPITCH); IS_A picks the layout, MODE says which axis the halves run along.
+template <int MODE, bool IS_A>
+__device__ inline void stage4(double* __restrict__ st, h4 v, int tid) {
+    constexpr int ROWS = IS_A ? HGEMM_BM : HGEMM_BN;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        int row, kk;
+        if constexpr (MODE == LOAD_MN) {
+            kk = tid / (ROWS / 4);
+            row = (tid % (ROWS / 4)) * 4 + e;
+        } else {
+            row = tid / (HGEMM_BK / 4);
+            kk = (tid % (HGEMM_BK / 4)) * 4 + e;
+        }
+        if constexpr (IS_A) st[row * APITCH + kk] = h2d(v[e]);
+        else st[kk * BPITCH + row] = h2d(v[e]);
+    }
+}
+
+template <int AM, int BMD>
+__global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
+    __shared__ double smem[2 * (A_STAGE + B_STAGE)];
+    double* As = smem;
+    double* Bs = smem + 2 * A_STAGE;
     uint32_t plane, tm, tn;
     gemm_detail::decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
     const uint32_t m0 = tm * HGEMM_BM, n0 = tn * HGEMM_BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lk = lane >> 4;
-    const uint16_t* A = p.a + static_cast<int64_t>(plane) * p.a_sb;
-    const uint16_t* B = p.b + static_cast<int64_t>(plane) * p.b_sb;
+    const uint16_t* A = p.a + static_cast<int64_t>(plane) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm;
+    const uint16_t* B = p.b + static_cast<int64_t>(plane) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn;
     uint16_t* C = p.c + static_cast<int64_t>(plane) * p.c_sb;
-    const bool inner = m0 + HGEMM_BM <= p.m && n0 + HGEMM_BN <= p.n;
+    const uint32_t mrem = p.m - m0, nrem = p.n - n0;
+    const bool inner = mrem >= HGEMM_BM && nrem >= HGEMM_BN;
 
     f64x4 acc[2][2];
 #pragma unroll
@@ -94,51 +154,43 @@ __global__ __launch_bounds__(HT) void gemm_f16_f64mfma(GemmHalfArgs p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
 
-    constexpr int LOADS = HGEMM_BM * HGEMM_BK / HT;  // 4 halves of A and 4 of B per thread
-    for (uint32_t k0 = 0; k0 < p.k; k0 += HGEMM_BK) {
-        uint16_t ra[LOADS], rb[LOADS];
+    h4 ra, rb;
+    auto load = [&](uint32_t k0) {
         if (inner && k0 + HGEMM_BK <= p.k) {
-#pragma unroll
-            for (int it = 0; it < LOADS; ++it) {
-                const int idx = it * HT + tid;
-                const int row = idx / HGEMM_BK, kk = idx % HGEMM_BK;
-                ra[it] = A[static_cast<int64_t>(m0 + row) * p.a_sm + static_cast<int64_t>(k0 + kk) * p.a_sk];
-                const int kb = idx / HGEMM_BN, col = idx % HGEMM_BN;
-                rb[it] = B[static_cast<int64_t>(k0 + kb) * p.b_sk + static_cast<int64_t>(n0 + col) * p.b_sn];
-            }
+            ra = load4<AM, true, HGEMM_BM>(A, p.a_sm, p.a_sk, mrem, k0, p.k, tid);
+            rb = load4<BMD, true, HGEMM_BN>(B, p.b_sn, p.b_sk, nrem, k0, p.k, tid);
         } else {
-#pragma unroll
-            for (int it = 0; it < LOADS; ++it) {
-                const int idx = it * HT + tid;
-                const int row = idx / HGEMM_BK, kk = idx % HGEMM_BK;
-                const bool ia = m0 + row < p.m && k0 + kk < p.k;
-                ra[it] = ia ? A[static_cast<int64_t>(m0 + row) * p.a_sm + static_cast<int64_t>(k0 + kk) * p.a_sk]
-                            : static_cast<uint16_t>(0);
-                const int kb = idx / HGEMM_BN, col = idx % HGEMM_BN;
-                const bool ib = k0 + kb < p.k && n0 + col < p.n;
-                rb[it] = ib ? B[static_cast<int64_t>(k0 + kb) * p.b_sk + static_cast<int64_t>(n0 + col) * p.b_sn]
-                            : static_cast<uint16_t>(0);
-            }
+            ra = load4<AM, false, HGEMM_BM>(A, p.a_sm, p.a_sk, mrem, k0, p.k, tid);
+            rb = load4<BMD, false, HGEMM_BN>(B, p.b_sn, p.b_sk, nrem, k0, p.k, tid);
         }
-#pragma unroll
-        for (int it = 0; it < LOADS; ++it) {
-            const int idx = it * HT + tid;
-            As[(idx / HGEMM_BK) * APITCH + idx % HGEMM_BK] = h2d(ra[it]);
-            Bs[(idx / HGEMM_BN) * BPITCH + idx % HGEMM_BN] = h2d(rb[it]);
-        }
-        __syncthreads();
+    };
+    const uint32_t ktiles = (p.k + HGEMM_BK - 1) / HGEMM_BK;
+    load(0);
+    stage4<AM, true>(As, ra, tid);
+    stage4<BMD, false>(Bs, rb, tid);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < ktiles; ++kt) {
+        const int s = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) load((kt + 1) * HGEMM_BK);
+        const double* as = As + s * A_STAGE;
+        const double* bs = Bs + s * B_STAGE;
 #pragma unroll
         for (int ks = 0; ks < HGEMM_BK / 4; ++ks) {
             double av[2], bv[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) av[i] = As[(wm * 32 + i * 16 + li) * APITCH + ks * 4 + lk];
+            for (int i = 0; i < 2; ++i) av[i] = as[(wm * 32 + i * 16 + li) * APITCH + ks * 4 + lk];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bv[j] = Bs[(ks * 4 + lk) * BPITCH + wn * 32 + j * 16 + li];
+            for (int j = 0; j < 2; ++j) bv[j] = bs[(ks * 4 + lk) * BPITCH + wn * 32 + j * 16 + li];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            stage4<AM, true>(As + (s ^ 1) * A_STAGE, ra, tid);
+            stage4<BMD, false>(Bs + (s ^ 1) * B_STAGE, rb, tid);
         }
         __syncthreads();
     }
@@ -222,9 +274,23 @@ uint64_t gemm_half_workgroups(uint32_t m, uint32_t n, uint32_t batch) {
     return static_cast<uint64_t>((m + HGEMM_BM - 1) / HGEMM_BM) * ((n + HGEMM_BN - 1) / HGEMM_BN) * batch;
 }
 
-void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args) {
-    const uint64_t g = gemm_half_workgroups(args.m, args.n, args.batch);
-    hipLaunchKernelGGL(gemm_f16_f64mfma, dim3(static_cast<uint32_t>(g)), dim3(HT), 0, s, args);
+void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int a_mode,
+                      int b_mode) {
+    const dim3 grid(static_cast<uint32_t>(gemm_half_workgroups(args.m, args.n, args.batch)));
+#define LG_HGEMM_CASE(AMV, BMV)                                                          \
+    if (a_mode == AMV && b_mode == BMV) {                                                \
+        hipLaunchKernelGGL((gemm_f16_f64mfma<AMV, BMV>), grid, dim3(HT), 0, s, args);    \
+    } else
+    LG_HGEMM_CASE(LOAD_K, LOAD_K)
+    LG_HGEMM_CASE(LOAD_K, LOAD_MN)
+    LG_HGEMM_CASE(LOAD_K, LOAD_S)
+    LG_HGEMM_CASE(LOAD_MN, LOAD_K)
+    LG_HGEMM_CASE(LOAD_MN, LOAD_MN)
+    LG_HGEMM_CASE(LOAD_MN, LOAD_S)
+    LG_HGEMM_CASE(LOAD_S, LOAD_K)
+    LG_HGEMM_CASE(LOAD_S, LOAD_MN)
+    LG_HGEMM_CASE(LOAD_S, LOAD_S) { fail_invalid("unknown operand load mode"); }
+#undef LG_HGEMM_CASE
     check_hip(hipGetLastError(), "gemm_f16_f64mfma");
     note_launch(ctx, "gemm_f16_f64mfma");
 }

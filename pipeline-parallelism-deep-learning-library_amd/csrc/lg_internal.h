@@ -192,7 +192,8 @@ struct FillHalfArgs {
     float beta;
     Axes4 c_batch, c_m, c_n;
 };
-void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args);
+void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int a_mode,
+                      int b_mode);
 void launch_general_half(Context* ctx, hipStream_t s, const GeneralHalfArgs& args);
 void launch_fill_half(Context* ctx, hipStream_t s, const FillHalfArgs& args);
 uint64_t gemm_half_workgroups(uint32_t m, uint32_t n, uint32_t batch);

@@ -377,8 +377,13 @@ def test_f16_plans_and_validation():
 
     a, b, c = hv(Layout.dense([64, 48])), hv(Layout.dense([48, 32])), hv(Layout.dense([64, 32]))
     p = C.plan_gemm(1.0, a, b, 0.0, c)
-    assert (p["kind"], p["a_mode"], p["b_mode"], p["splits"]) == ("tiled", "strided", "strided", 1)
+    assert (p["kind"], p["a_mode"], p["b_mode"], p["splits"]) == ("tiled", "k", "mn", 1)
     assert p["workgroups"] == 1
+    # 64-bit loads need 8-byte alignment and row strides in multiples of four halves.
+    p = C.plan_gemm(1.0, hv(Layout.dense([64, 46])), hv(Layout.transposed(46, 32)), 0.0, c)
+    assert (p["a_mode"], p["b_mode"]) == ("strided", "strided")
+    p = C.plan_gemm(1.0, hv(Layout.transposed(64, 48)), hv(Layout.transposed(48, 32)), 0.0, c)
+    assert (p["a_mode"], p["b_mode"]) == ("mn", "k")
     assert C.plan_gemm(0.0, a, b, 0.0, c)["kind"] == "zero"
     assert C.plan_gemm(0.0, a, b, 0.5, c)["kind"] == "scale"
     # Tall K never splits on the f16 path (one f64 tile per output block).

@@ -106,6 +106,43 @@ def test_transposed_operands_are_read_in_place(ctx, pool, at, bt):
     assert f16_bits_equal(c.read()[: m * n].reshape(m, n), want)
 
 
+def _mode_layout(operand, mode, rows, cols):
+    """A [rows, cols] view of A (rows = M, cols = K) or B (rows = K, cols = N) whose plan
+    takes `mode`: "k" or "mn" unit stride along that axis with 8-byte alignment, "strided"
+    the same storage shifted by one element (misaligned for 64-bit loads)."""
+    contiguous_cols = (operand == "a") == (mode != "mn")
+    lay = Layout.dense([rows, cols]) if contiguous_cols else Layout.transposed(rows, cols)
+    if mode == "strided":
+        lay = Layout(1, lay.shape, lay.strides)
+    return lay
+
+
+@pytest.mark.parametrize("amode", ["k", "mn", "strided"])
+@pytest.mark.parametrize("bmode", ["k", "mn", "strided"])
+def test_every_load_mode_pair_rounds_once(ctx, pool, amode, bmode):
+    """Each operand layout the tile kernel loads differently (64-bit loads along K, along M/N,
+    or predicated 16-bit loads) on a ragged 68x132x40 product. Halves on the 2^-10 grid keep
+    every partial sum exact in f64 (|sum| < 2^8 in steps of 2^-20), and alpha = -1/2,
+    beta = 1/4 keep alpha*sum + beta*c exact, so numpy's correctly rounded f64 -> f16
+    conversion of the f64 result is the exact value rounded once: bit for bit."""
+    m, n, k = 68, 132, 40
+    g = rng(11 + 3 * ["k", "mn", "strided"].index(amode) + ["k", "mn", "strided"].index(bmode))
+    la, lb = _mode_layout("a", amode, m, k), _mode_layout("b", bmode, k, n)
+    a = Half(pool, la, grid_halves(g, la.span()))
+    b = Half(pool, lb, grid_halves(g, lb.span()))
+    c = Half(pool, Layout.dense([m, n]), grid_halves(g, m * n))
+    before = c.read()
+    plan = C.plan_gemm(-0.5, a.view(), b.view(), 0.25, c.view())
+    assert (plan["kind"], plan["a_mode"], plan["b_mode"]) == ("tiled", amode, bmode), plan
+    C.gemm(ctx, -0.5, a.view(), b.view(), 0.25, c.view())
+    exact = (-0.5 * (a.logical().astype(np.float64) @ b.logical().astype(np.float64))
+             + 0.25 * c.logical().astype(np.float64))
+    want = exact.astype(np.float16).view(np.uint16)
+    got = c.read()
+    assert f16_bits_equal(got[: m * n].reshape(m, n), want)
+    assert np.array_equal(got[m * n:].view(np.uint16), before[m * n:].view(np.uint16))
+
+
 def gate_check(name, got, exact, magnitude, k):
     rounded = exact.astype(np.float16).astype(np.float64)
     fin = np.isfinite(rounded)
