@@ -105,7 +105,8 @@ def test_bias_grad_is_the_sequential_column_sum(hb, rows, cols):
     assert len(hb.debug_launches()) == n0
 
 
-@pytest.mark.parametrize("shape", [(8, 65), (1, 1), (3, 5), (1024, 1024), (4097, 33)])
+@pytest.mark.parametrize("shape", [(8, 65), (1, 1), (3, 5), (1024, 1024), (4097, 33),
+                                   (2049, 2052), (2049, 2051)])
 def test_mse_grad(hb, shape):
     n = int(np.prod(shape))
     g = rng(n)
