@@ -348,7 +348,7 @@ def main() -> int:
                          "of sustained MFMA load to reach its steady clock (5 launches of the "
                          "4096^3 GEMM measure ~7%% below steady state)")
     ap.add_argument("--only", default=None,
-                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, train, f16")
+                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, t8191, train, f16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -417,6 +417,16 @@ def main() -> int:
                                   [512, 1024, 256], [2, 0, 1], 4, args))
     run("copy", lambda: {"name": "plain 128-bit copy 512 MiB", "gbs": bench_copy(ctx, events, pool,
                                                                                  L, P, 1 << 27, args)})
+    def t8191():
+        # The reference's transpose benchmark (tests/permutation_test.rs:741-792): an
+        # 8191x4099 f32 transpose against a plain copy of the same bytes; it asserts >= 70 %.
+        r = bench_perm(ctx, events, pool, L, P, "transpose [8191,4099] perm (1,0)", [8191, 4099],
+                       [1, 0], 3000, args)
+        r.pop("_host")
+        r["copy_gbs"] = bench_copy(ctx, events, pool, L, P, 8191 * 4099, args)
+        r["ratio_vs_copy"] = r["gbs"] / r["copy_gbs"]
+        return r
+    run("t8191", t8191)
     run("train", lambda: bench_train_ops(events, args, timed))
     run("f16", lambda: bench_gemm_f16(ctx, events, pool, L, C, 4096, 4096, 4096, args))
 

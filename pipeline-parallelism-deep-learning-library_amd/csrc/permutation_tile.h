@@ -76,10 +76,37 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
         // allowed. Then every load of the fill is issued before the first one is waited on,
         // and the drain reads all its LDS words before its stores, with no per-chunk
         // branches to serialize the memory pipeline.
-        const bool full = VEC && a0 + TA <= p.ext_a && b0 + TB <= p.ext_b;
+        const bool inside = a0 + TA <= p.ext_a && b0 + TB <= p.ext_b;
+        const bool full = VEC && inside;
+        // A view that 128-bit accesses cannot serve (rows not 16-byte aligned, such as an odd
+        // row pitch) still takes a branch-free path for interior tiles: 32-bit accesses with
+        // lane i on word i of a row, so each wave instruction covers 256 contiguous bytes.
+        constexpr int ROW_WORDS = TA * W;   // words of one tile row in the source (along a)
+        constexpr int COL_WORDS = TB * W;   // words of one destination row segment (along b)
+        constexpr int WORDS_IN = TB * ROW_WORDS / PERM_THREADS;
+        constexpr int WORDS_OUT = TA * COL_WORDS / PERM_THREADS;
+        static_assert(WORDS_IN * PERM_THREADS == TB * ROW_WORDS, "word fill must split evenly");
+        static_assert(WORDS_OUT * PERM_THREADS == TA * COL_WORDS, "word drain must split evenly");
+        const bool words_full = !VEC && inside;
 
         // Fill: rows of the tile are b, 128-bit chunks run along a.
-        if (full) {
+        if (words_full) {
+            if constexpr (!VEC) {
+                uint32_t r[WORDS_IN];
+#pragma unroll
+                for (int it = 0; it < WORDS_IN; ++it) {
+                    const int idx = it * PERM_THREADS + tid;
+                    const int bb = idx / ROW_WORDS, cw = idx % ROW_WORDS;
+                    const int64_t e0 = sbase + static_cast<int64_t>(b0 + bb) * p.src_sb + a0;
+                    r[it] = src[e0 * W + cw];
+                }
+#pragma unroll
+                for (int it = 0; it < WORDS_IN; ++it) {
+                    const int idx = it * PERM_THREADS + tid;
+                    tile[(idx / ROW_WORDS) * PITCH + idx % ROW_WORDS] = r[it];
+                }
+            }
+        } else if (full) {
             u32x4 r[FILL_ITERS];
 #pragma unroll
             for (int it = 0; it < FILL_ITERS; ++it) {
@@ -139,7 +166,27 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             }
             return v;
         };
-        if (full) {
+        if (words_full) {
+            if constexpr (!VEC) {
+                uint32_t v[WORDS_OUT];
+#pragma unroll
+                for (int it = 0; it < WORDS_OUT; ++it) {
+                    const int idx = it * PERM_THREADS + tid;
+                    const int aa = idx / COL_WORDS, cwb = idx % COL_WORDS;
+                    const int w = cwb % W;
+                    uint32_t word = tile[(cwb / W) * PITCH + aa * W + w];
+                    if (CONJ && w == 1) word ^= SIGN;
+                    v[it] = word;
+                }
+#pragma unroll
+                for (int it = 0; it < WORDS_OUT; ++it) {
+                    const int idx = it * PERM_THREADS + tid;
+                    const int aa = idx / COL_WORDS, cwb = idx % COL_WORDS;
+                    const int64_t e0 = dbase + static_cast<int64_t>(a0 + aa) * p.dst_sa + b0;
+                    dst[e0 * W + cwb] = v[it];
+                }
+            }
+        } else if (full) {
             u32x4 v[DRAIN_ITERS];
 #pragma unroll
             for (int it = 0; it < DRAIN_ITERS; ++it) {

@@ -154,7 +154,8 @@ def check_involution(ctx, pool, dtype, batch, m, n, seed):
 
 def test_adjoint_twice_is_bitwise_identity_with_special_values(ctx, pool):
     shapes = [([], 1, 1), ([], 1, 7), ([], 7, 1), ([], 32, 32), ([], 31, 33), ([], 67, 101),
-              ([], 129, 65), ([3], 5, 37), ([2, 3], 41, 7), ([7], 33, 1), ([2], 64, 128)]
+              ([], 129, 65), ([3], 5, 37), ([2, 3], 41, 7), ([7], 33, 1), ([2], 64, 128),
+              ([2], 301, 203)]
     for i, (batch, m, n) in enumerate(shapes):
         check_involution(ctx, pool, "f32", batch, m, n, 1000 + i)
         check_involution(ctx, pool, "c64", batch, m, n, 1100 + i)
