@@ -53,6 +53,10 @@ class HipEvents:
         assert self.hip.hipEventCreate(ctypes.byref(ev)) == 0
         return ev
 
+    def destroy(self, *evs):
+        for ev in evs:
+            assert self.hip.hipEventDestroy(ev) == 0
+
     def record(self, ev, stream):
         assert self.hip.hipEventRecord(ev, stream) == 0
 
@@ -83,12 +87,29 @@ def timed(ctx, events, launch, steps, warmup):
     events.record(e1, s)
     total = events.elapsed_ms(e0, e1)
     ctx.sync()
+    events.destroy(e0, e1)
     return total / steps
 
 
 def native_lib():
     from linalg_hip import _native
     return _native.lib()
+
+
+def per_launch(ctx, events, launch, n):
+    """(median, best) ms of `n` launches each bracketed by its own event pair, taken after the
+    timed loop (the way tests/contraction_test.rs:1199-1217 reports best and median)."""
+    s = ctx.queue.handle
+    pairs = [(events.new(), events.new()) for _ in range(n)]
+    for a, b in pairs:
+        events.record(a, s)
+        launch()
+        events.record(b, s)
+    ms = sorted(events.elapsed_ms(a, b) for a, b in pairs)
+    ctx.sync()
+    for a, b in pairs:
+        events.destroy(a, b)
+    return ms[len(ms) // 2], ms[0]
 
 
 def abi_call(fn, *args):
@@ -134,9 +155,11 @@ def bench_gemm(ctx, events, pool, L, C, name, m, n, k, args, a_t=False, b_t=Fals
     launch = abi_call(native_lib().lg_encode_gemm_f32, ctx.handle, ctx.queue.handle,
                       ctypes.c_float(1.0), av.to_c(), bv.to_c(), ctypes.c_float(beta), cv.to_c())
     ms = timed(ctx, events, launch, args.steps, args.warmup)
+    med, best = per_launch(ctx, events, launch, args.steps)
     flops = 2.0 * batch * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"name": name, "ms": ms, "host_ms": HOST_MS[launch], "tflops": tflops,
+    return {"name": name, "ms": ms, "ms_median": med, "ms_best": best,
+            "host_ms": HOST_MS[launch], "tflops": tflops,
             "frac": tflops / PEAK_TFLOPS,
             "plan": {k_: plan[k_] for k_ in ("kind", "a_mode", "b_mode", "splits", "workgroups")},
             "_host": (a, b)}
@@ -154,8 +177,10 @@ def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
     launch = abi_call(native_lib().lg_encode_materialize, ctx.handle, ctx.queue.handle, src.elem,
                       src.to_c(), dst.to_c())
     ms = timed(ctx, events, launch, args.steps, args.warmup)
+    med, best = per_launch(ctx, events, launch, args.steps)
     gbs = 2.0 * n * 4 / (ms * 1e-3) / 1e9
-    return {"name": name, "ms": ms, "host_ms": HOST_MS[launch], "gbs": gbs, "frac": gbs / PEAK_GBS,
+    return {"name": name, "ms": ms, "ms_median": med, "ms_best": best,
+            "host_ms": HOST_MS[launch], "gbs": gbs, "frac": gbs / PEAK_GBS,
             "plan": {k_: plan[k_] for k_ in ("kind", "vector", "workgroups", "shape")},
             "_host": x}
 
