@@ -374,8 +374,10 @@ typedef struct lg_contract_plan {
     uint64_t k_chunk;     /* K elements per split */
     uint64_t workgroups;  /* workgroups of the main launch */
     uint64_t scratch_bytes; /* device scratch of the split-K partials */
-    uint32_t tile_m;      /* output tile of one workgroup (tiled/split): 128x128, or 64x64 when */
-    uint32_t tile_n;      /* 128x128 tiles would leave most compute units idle; f16: 64x64 */
+    uint32_t tile_m;      /* output tile of one workgroup (tiled/split): 128x128; 64x64 when */
+    uint32_t tile_n;      /* 128x128 tiles would leave most compute units idle; 32x32 (one
+                             launch, the four waves splitting K) for small outputs with
+                             K <= 1024; f16: 64x64 */
 } lg_contract_plan;
 
 lg_status lg_plan_contract_f32(float alpha, const lg_view* a, const char* a_labels,

@@ -623,7 +623,13 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     const uint64_t big = static_cast<uint64_t>((m + GEMM_BM - 1) / GEMM_BM) *
                          ((n + GEMM_BN - 1) / GEMM_BN) * batch;
     const uint64_t k_ways = std::max<uint64_t>(1, std::min<uint64_t>(k / SPLIT_MIN_CHUNK, SPLIT_MAX));
-    t.tile = big * k_ways < GEMM_SMALL_BELOW ? GEMM_SMALL_TILE : GEMM_BM;
+    const uint64_t mid = static_cast<uint64_t>((m + GEMM_SMALL_TILE - 1) / GEMM_SMALL_TILE) *
+                         ((n + GEMM_SMALL_TILE - 1) / GEMM_SMALL_TILE) * batch;
+    if (mid < GEMM_SMALL_BELOW && k <= GEMM_SMALL_K) {
+        t.tile = GEMM_TINY_TILE;  // one launch, no split-K partials
+    } else {
+        t.tile = big * k_ways < GEMM_SMALL_BELOW ? GEMM_SMALL_TILE : GEMM_BM;
+    }
     t.tiles_m = (m + t.tile - 1) / t.tile;
     t.tiles_n = (n + t.tile - 1) / t.tile;
     info.tile_m = info.tile_n = t.tile;
@@ -633,7 +639,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     info.b_mode = static_cast<uint32_t>(b_mode);
     const uint64_t tiles = static_cast<uint64_t>(t.tiles_m) * t.tiles_n * batch;
     uint32_t splits = 1, chunk = k;
-    split_shape(tiles, k, &splits, &chunk);
+    if (t.tile != GEMM_TINY_TILE) split_shape(tiles, k, &splits, &chunk);
     if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
     t.splits = splits;
     t.k_chunk = chunk;

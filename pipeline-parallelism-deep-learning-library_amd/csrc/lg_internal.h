@@ -117,6 +117,13 @@ constexpr uint32_t GEMM_BN = 128;
 #endif
 constexpr uint32_t GEMM_SMALL_TILE = 64;
 constexpr uint64_t GEMM_SMALL_BELOW = LG_GEMM_SMALL_BELOW;
+// Products whose 64x64 grid is under GEMM_SMALL_BELOW tiles and whose K is at most
+// GEMM_SMALL_K take the single-launch 32x32 kernel (gemm_f32_small) instead of split-K.
+#ifndef LG_GEMM_SMALL_K
+#define LG_GEMM_SMALL_K 1024
+#endif
+constexpr uint32_t GEMM_TINY_TILE = 32;
+constexpr uint32_t GEMM_SMALL_K = LG_GEMM_SMALL_K;
 constexpr uint32_t GEMM_BK = 16;       // K-slice depth per LDS stage
 constexpr uint32_t GEMM_THREADS = 256;
 
@@ -132,7 +139,7 @@ struct GemmArgs {
     uint32_t k_chunk, splits;
     uint32_t tiles_m, tiles_n;
     float alpha, beta;
-    uint32_t tile;  // output tile edge: GEMM_BM (128) or GEMM_SMALL_TILE (64)
+    uint32_t tile;  // output tile edge: GEMM_BM (128), GEMM_SMALL_TILE (64) or GEMM_TINY_TILE (32)
 };
 
 struct ReduceArgs {

@@ -220,6 +220,9 @@ def test_output_tile_choice():
     assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (128, 128), 289)
     p = C.plan_gemm(1.0, dense([1900, 45]), dense([45, 1950]), 0.0, dense([1900, 1950]))
     assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (64, 64), 30 * 31)
+    # Small output, short K: one launch of 32x32 tiles.
+    p = C.plan_gemm(1.0, dense([130, 300]), dense([300, 250]), 0.0, dense([130, 250]))
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (32, 32), 5 * 8)
     # Small output, long K: 64x64 tiles, then split-K up to the workgroup target.
     p = C.plan_gemm(1.0, dense([200, 2000]), dense([2000, 190]), 0.0, dense([200, 190]))
     assert (p["kind"], p["tile"]) == ("split", (64, 64))
@@ -232,7 +235,8 @@ def test_output_tile_choice():
 def test_contraction_plans_for_the_baseline_configs():
     p = C.plan_gemm(1.0, dense([512, 512]), dense([512, 512]), 0.0, dense([512, 512]))
     assert p["kind"] in ("tiled", "split") and p["a_mode"] == "k" and p["b_mode"] == "mn"
-    assert p["tile"] == (64, 64)  # 16 tiles of 128x128 would leave most of the chip idle
+    # 16 tiles of 128x128 would leave most of the chip idle: 32x32 tiles in one launch.
+    assert p["kind"] == "tiled" and p["tile"] == (32, 32) and p["workgroups"] == 256
     # Config 3: B given as a permuted view "bkj" of [32, j, k] storage (unit stride along k).
     bstore = dense([32, 1024, 1024])
     bview = P.permute_view(bstore, [0, 2, 1])
