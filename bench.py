@@ -493,7 +493,7 @@ def main() -> int:
                                         "peak": PEAK_GBS, "unit": "GB/s",
                                         "frac": round(perm["frac"], 4),
                                         "traffic": traffic_from_profile("c2b"),
-                                        "kernel": "perm_tile<1, false, true, 128, 64, 3> (non-temporal loads and stores)",
+                                        "kernel": "perm_tile<1, false, true, 128, 64, 3, 256> (non-temporal loads and stores)",
                                         "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
                                         "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
                            "cpu_baseline": cpu["permute"] if cpu else None}

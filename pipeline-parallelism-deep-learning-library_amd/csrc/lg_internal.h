@@ -222,7 +222,8 @@ constexpr uint32_t PERM_TILE_B = 64;   // transpose tile extent along b (destina
 // tiles are twice as long along the source rows).
 constexpr uint32_t PERM_STREAM_TILE_A = 128;
 constexpr uint64_t PERM_STREAM_BYTES = 256ull << 20;
-constexpr uint32_t PERM_THREADS = 256;
+constexpr uint32_t PERM_THREADS = 256;         // copy kernel and streaming transpose tiles
+constexpr uint32_t PERM_CACHED_THREADS = 512;  // transpose tiles that stay in the cache
 
 struct PermTileArgs {
     const void* src;  // allocation bases

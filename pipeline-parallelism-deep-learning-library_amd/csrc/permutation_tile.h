@@ -39,17 +39,17 @@ __device__ inline void store128(uint32_t* p, u32x4 v) {
     else *reinterpret_cast<u32x4*>(p) = v;
 }
 
-template <int W, bool CONJ, bool VEC, int TA, int TB, int NTM = 0>
-__global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
+template <int W, bool CONJ, bool VEC, int TA, int TB, int NTM, int NTH>
+__global__ __launch_bounds__(NTH) void perm_tile(PermTileArgs p) {
     constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;
     constexpr int VE = 4 / W;                       // elements per 128-bit word
     constexpr int PITCH = TA * W + 1;               // LDS row pitch in words (rows are b)
     constexpr int FILL_CHUNKS = TA * W / 4;         // 128-bit chunks per tile row (along a)
     constexpr int DRAIN_CHUNKS = TB * W / 4;        // 128-bit chunks per output row (along b)
-    constexpr int FILL_ITERS = TB * FILL_CHUNKS / PERM_THREADS;
-    constexpr int DRAIN_ITERS = TA * DRAIN_CHUNKS / PERM_THREADS;
-    static_assert(FILL_ITERS * PERM_THREADS == TB * FILL_CHUNKS, "fill must split evenly");
-    static_assert(DRAIN_ITERS * PERM_THREADS == TA * DRAIN_CHUNKS, "drain must split evenly");
+    constexpr int FILL_ITERS = TB * FILL_CHUNKS / NTH;
+    constexpr int DRAIN_ITERS = TA * DRAIN_CHUNKS / NTH;
+    static_assert(FILL_ITERS * NTH == TB * FILL_CHUNKS, "fill must split evenly");
+    static_assert(DRAIN_ITERS * NTH == TA * DRAIN_CHUNKS, "drain must split evenly");
     __shared__ uint32_t tile[TB * PITCH];
 
     const uint32_t* src = static_cast<const uint32_t*>(p.src);
@@ -83,10 +83,10 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
         // lane i on word i of a row, so each wave instruction covers 256 contiguous bytes.
         constexpr int ROW_WORDS = TA * W;   // words of one tile row in the source (along a)
         constexpr int COL_WORDS = TB * W;   // words of one destination row segment (along b)
-        constexpr int WORDS_IN = TB * ROW_WORDS / PERM_THREADS;
-        constexpr int WORDS_OUT = TA * COL_WORDS / PERM_THREADS;
-        static_assert(WORDS_IN * PERM_THREADS == TB * ROW_WORDS, "word fill must split evenly");
-        static_assert(WORDS_OUT * PERM_THREADS == TA * COL_WORDS, "word drain must split evenly");
+        constexpr int WORDS_IN = TB * ROW_WORDS / NTH;
+        constexpr int WORDS_OUT = TA * COL_WORDS / NTH;
+        static_assert(WORDS_IN * NTH == TB * ROW_WORDS, "word fill must split evenly");
+        static_assert(WORDS_OUT * NTH == TA * COL_WORDS, "word drain must split evenly");
         const bool words_full = !VEC && inside;
 
         // Fill: rows of the tile are b, 128-bit chunks run along a.
@@ -95,14 +95,14 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
                 uint32_t r[WORDS_IN];
 #pragma unroll
                 for (int it = 0; it < WORDS_IN; ++it) {
-                    const int idx = it * PERM_THREADS + tid;
+                    const int idx = it * NTH + tid;
                     const int bb = idx / ROW_WORDS, cw = idx % ROW_WORDS;
                     const int64_t e0 = sbase + static_cast<int64_t>(b0 + bb) * p.src_sb + a0;
                     r[it] = src[e0 * W + cw];
                 }
 #pragma unroll
                 for (int it = 0; it < WORDS_IN; ++it) {
-                    const int idx = it * PERM_THREADS + tid;
+                    const int idx = it * NTH + tid;
                     tile[(idx / ROW_WORDS) * PITCH + idx % ROW_WORDS] = r[it];
                 }
             }
@@ -110,14 +110,14 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             u32x4 r[FILL_ITERS];
 #pragma unroll
             for (int it = 0; it < FILL_ITERS; ++it) {
-                const int idx = it * PERM_THREADS + tid;
+                const int idx = it * NTH + tid;
                 const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
                 const int64_t e0 = sbase + static_cast<int64_t>(b0 + bb) * p.src_sb + a0 + cw / W;
                 r[it] = load128<NTL>(src + e0 * W);
             }
 #pragma unroll
             for (int it = 0; it < FILL_ITERS; ++it) {
-                const int idx = it * PERM_THREADS + tid;
+                const int idx = it * NTH + tid;
                 const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;
                 uint32_t* row = tile + bb * PITCH + cw;
                 row[0] = r[it][0];
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
         } else {
 #pragma unroll
             for (int it = 0; it < FILL_ITERS; ++it) {
-                const int idx = it * PERM_THREADS + tid;
+                const int idx = it * NTH + tid;
                 const int bb = idx / FILL_CHUNKS, cw = (idx % FILL_CHUNKS) * 4;  // word column
                 const uint32_t a = a0 + cw / W, b = b0 + bb;
                 uint32_t* row = tile + bb * PITCH + cw;
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
                 uint32_t v[WORDS_OUT];
 #pragma unroll
                 for (int it = 0; it < WORDS_OUT; ++it) {
-                    const int idx = it * PERM_THREADS + tid;
+                    const int idx = it * NTH + tid;
                     const int aa = idx / COL_WORDS, cwb = idx % COL_WORDS;
                     const int w = cwb % W;
                     uint32_t word = tile[(cwb / W) * PITCH + aa * W + w];
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
                 }
 #pragma unroll
                 for (int it = 0; it < WORDS_OUT; ++it) {
-                    const int idx = it * PERM_THREADS + tid;
+                    const int idx = it * NTH + tid;
                     const int aa = idx / COL_WORDS, cwb = idx % COL_WORDS;
                     const int64_t e0 = dbase + static_cast<int64_t>(a0 + aa) * p.dst_sa + b0;
                     dst[e0 * W + cwb] = v[it];
@@ -190,12 +190,12 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
             u32x4 v[DRAIN_ITERS];
 #pragma unroll
             for (int it = 0; it < DRAIN_ITERS; ++it) {
-                const int idx = it * PERM_THREADS + tid;
+                const int idx = it * NTH + tid;
                 v[it] = gather(idx / DRAIN_CHUNKS, (idx % DRAIN_CHUNKS) * 4 / W);
             }
 #pragma unroll
             for (int it = 0; it < DRAIN_ITERS; ++it) {
-                const int idx = it * PERM_THREADS + tid;
+                const int idx = it * NTH + tid;
                 const int aa = idx / DRAIN_CHUNKS, bl = (idx % DRAIN_CHUNKS) * 4 / W;
                 const int64_t e0 = dbase + static_cast<int64_t>(a0 + aa) * p.dst_sa + b0 + bl;
                 store128<NTS>(dst + e0 * W, v[it]);
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_tile(PermTileArgs p) {
         } else {
 #pragma unroll
             for (int it = 0; it < DRAIN_ITERS; ++it) {
-                const int idx = it * PERM_THREADS + tid;
+                const int idx = it * NTH + tid;
                 const int aa = idx / DRAIN_CHUNKS, cw = (idx % DRAIN_CHUNKS) * 4;
                 const int bl = cw / W;  // first b (local) of this chunk
                 const uint32_t a = a0 + aa, b = b0 + bl;

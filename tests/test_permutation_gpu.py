@@ -362,6 +362,26 @@ def test_baseline_configs_full_size_bit_exact(ctx, pool, shape, perm, seed):
     assert np.array_equal(back_buf.read(np.uint32, count=n), x.view(np.uint32))
 
 
+def test_transpose_reads_misaligned_rows_to_the_edges_of_the_buffer(ctx, pool):
+    """A view whose rows are not 16-byte aligned, in a buffer that starts 4 bytes into a device
+    allocation and ends at the view's last word: interior and edge tiles move every word once
+    and touch nothing outside the view, for one-word and two-word (complex) elements."""
+    for dtype, (m, n) in (("f32", (131, 1031)), ("c64", (67, 261))):
+        words_per = 2 if dtype == "c64" else 1
+        real = pool.alloc("f32", (m * n + 8) * words_per)
+        buf = L.Buffer(ctx, real.base + 4, m * n * 4 * words_per)
+        host = random_words(rng(m + n), m * n * words_per)
+        buf.write(host)
+        src = L.TensorView.row_major(buf, 0, [m, n], dtype)
+        dst_buf = pool.alloc(dtype, m * n)
+        dst = L.TensorView.row_major(dst_buf, 0, [n, m], dtype)
+        plan = P.plan("materialize", P.permute_view(src, [1, 0]), dst)
+        assert plan["kind"] == "tile" and not plan["vector"], plan
+        P.materialize(ctx, P.permute_view(src, [1, 0]), dst)
+        want = host.reshape(m, n, words_per).transpose(1, 0, 2).ravel()
+        assert np.array_equal(dst_buf.read(np.uint32, count=m * n * words_per), want), dtype
+
+
 def test_transpose_8191x4099_against_copy_spot_check(ctx, pool):
     """The reference benchmark's shape (permutation_test.rs:741-792), checked word for word."""
     m, n = 8191, 4099
