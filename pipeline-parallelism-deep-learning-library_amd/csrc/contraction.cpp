@@ -404,11 +404,11 @@ struct Plan {
     FillHalfArgs hfill{};
 };
 
-// 64-bit loads of four halves need the view's first element 8-byte aligned and every other
-// stride a multiple of four elements.
+// 128-bit loads of eight halves need the view's first element 16-byte aligned and every other
+// stride a multiple of eight elements.
 int load_mode_half(uintptr_t base, uint64_t off, uint64_t sb, uint64_t srow, uint64_t sk) {
-    auto al = [](uint64_t x) { return x % 4 == 0; };
-    const bool start = (base + off * 2) % 8 == 0;
+    auto al = [](uint64_t x) { return x % 8 == 0; };
+    const bool start = (base + off * 2) % 16 == 0;
     if (sk == 1 && start && al(srow) && al(sb)) return LOAD_K;
     if (srow == 1 && start && al(sk) && al(sb)) return LOAD_MN;
     return LOAD_S;

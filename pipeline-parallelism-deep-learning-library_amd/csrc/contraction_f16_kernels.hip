@@ -68,74 +68,76 @@ __device__ inline uint16_t finish(double acc, float alpha, float beta, const uin
 // v_mfma_f64_16x16x4_f64. Block operand layout (checked on gfx950): A lane l holds row l%16,
 // k l/16; B lane l holds column l%16, k l/16; accumulator value v of lane l is row 4*v + l/16,
 // column l%16 (rows interleave across the four 16-lane groups).
-// K advances 16 at a time through two LDS stages of f64: while the MFMAs consume stage s, the
-// next slice is in flight from memory into registers (four halves per thread and operand, one
-// 64-bit load when the operand is contiguous along the tile's short axis), and is widened and
-// written to stage s^1 before the one barrier per slice. 34 KB of LDS and under 128 VGPRs
-// keep four workgroups on a compute unit.
+// K advances 64 at a time through two LDS stages that hold the halves as they are (the f64
+// values are formed when a fragment is read, exactly), so a 64-deep slice costs 18 KB per
+// stage and each barrier serves 64 MFMAs per wave. While the MFMAs consume stage s, the next
+// slice is in flight into registers: two 128-bit loads of eight halves per thread and operand
+// when the operand is contiguous along K (stage [row][k]) or along M/N (stage [k][row]),
+// predicated 16-bit loads otherwise. 36 KB of LDS keeps four workgroups on a compute unit.
 constexpr int HT = 256;
-constexpr int APITCH = HGEMM_BK + 1;  // doubles; odd pitch spreads the k-column reads
-constexpr int BPITCH = HGEMM_BN + 1;
-constexpr int A_STAGE = HGEMM_BM * APITCH;
-constexpr int B_STAGE = HGEMM_BK * BPITCH;
-static_assert(HGEMM_BM * HGEMM_BK == 4 * HT && HGEMM_BN * HGEMM_BK == 4 * HT,
-              "each thread stages four halves of A and four of B per slice");
+constexpr int HP = HGEMM_BK + 8;        // halves per stage row: 128-bit rows stay 16-byte aligned
+constexpr int H_STAGE = HGEMM_BM * HP;  // halves per operand stage (both operands are 64 x 64)
+constexpr int HCH = HGEMM_BM * HGEMM_BK / 8 / HT;  // 128-bit chunks per thread and operand
+static_assert(HGEMM_BM == 64 && HGEMM_BN == 64 && HGEMM_BK == 64, "stage geometry");
+static_assert(HCH * HT * 8 == HGEMM_BM * HGEMM_BK, "each thread stages whole chunks");
 
-typedef uint16_t h4 __attribute__((ext_vector_type(4)));
+typedef uint16_t h8 __attribute__((ext_vector_type(8)));
 
-// Four halves of one operand's K-slice for thread `tid`. `p` is (row 0, k 0) of the tile,
-// srow/sk its strides; the thread's halves run along k (LOAD_K, LOAD_S) or along the row axis
+// One operand's K-slice for thread `tid`: HCH runs of eight halves. `p` is (row 0, k 0) of the
+// tile, srow/sk its strides; the runs go along k (LOAD_K, LOAD_S) or along the row axis
 // (LOAD_MN). FULL: the slice lies inside the operand, so no predicates.
-template <int MODE, bool FULL, int ROWS>
-__device__ inline h4 load4(const uint16_t* __restrict__ p, int64_t srow, int64_t sk,
-                           uint32_t rows_left, uint32_t k0, uint32_t klen, int tid) {
-    h4 r;
-    if constexpr (MODE == LOAD_MN) {
-        const uint32_t kr = k0 + tid / (ROWS / 4), row = (tid % (ROWS / 4)) * 4;
-        const uint16_t* q = p + static_cast<int64_t>(kr) * sk + row;
-        if (FULL) return *reinterpret_cast<const h4*>(q);
+template <int MODE, bool FULL>
+__device__ inline void hload(h8 (&r)[HCH], const uint16_t* __restrict__ p, int64_t srow,
+                             int64_t sk, uint32_t rows_left, uint32_t k0, uint32_t klen,
+                             int tid) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (kr < klen && row + e < rows_left) ? q[e] : uint16_t(0);
-    } else {
-        const uint32_t row = tid / (HGEMM_BK / 4), kk = k0 + (tid % (HGEMM_BK / 4)) * 4;
-        const uint16_t* q = p + static_cast<int64_t>(row) * srow;
-        if constexpr (MODE == LOAD_K) {
-            if (FULL) return *reinterpret_cast<const h4*>(q + kk);
-        }
+    for (int it = 0; it < HCH; ++it) {
+        const int idx = it * HT + tid;
+        if constexpr (MODE == LOAD_MN) {
+            const uint32_t kr = k0 + idx / 8, row = (idx % 8) * 8;
+            const uint16_t* q = p + static_cast<int64_t>(kr) * sk + row;
+            if (FULL) {
+                r[it] = *reinterpret_cast<const h8*>(q);
+            } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            r[e] = (FULL || (row < rows_left && kk + e < klen))
-                       ? q[static_cast<int64_t>(kk + e) * sk] : uint16_t(0);
+                for (int e = 0; e < 8; ++e) r[it][e] = (kr < klen && row + e < rows_left) ? q[e] : uint16_t(0);
+            }
+        } else {
+            const uint32_t row = idx / 8, kk = k0 + (idx % 8) * 8;
+            const uint16_t* q = p + static_cast<int64_t>(row) * srow;
+            if (MODE == LOAD_K && FULL) {
+                r[it] = *reinterpret_cast<const h8*>(q + kk);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    r[it][e] = (FULL || (row < rows_left && kk + e < klen))
+                                   ? q[static_cast<int64_t>(kk + e) * sk] : uint16_t(0);
+                }
+            }
         }
     }
-    return r;
 }
 
-// Widens the four halves and writes them to the stage: A as [row][k] (pitch APITCH), B as
-// [k][col] (pitch BPITCH); IS_A picks the layout, MODE says which axis the halves run along.
-template <int MODE, bool IS_A>
-__device__ inline void stage4(double* __restrict__ st, h4 v, int tid) {
-    constexpr int ROWS = IS_A ? HGEMM_BM : HGEMM_BN;
+// Writes the runs to a stage: [k][row] for LOAD_MN, [row][k] otherwise (pitch HP halves).
+__device__ inline void hstage(uint16_t* __restrict__ st, const h8 (&r)[HCH], int tid) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        int row, kk;
-        if constexpr (MODE == LOAD_MN) {
-            kk = tid / (ROWS / 4);
-            row = (tid % (ROWS / 4)) * 4 + e;
-        } else {
-            row = tid / (HGEMM_BK / 4);
-            kk = (tid % (HGEMM_BK / 4)) * 4 + e;
-        }
-        if constexpr (IS_A) st[row * APITCH + kk] = h2d(v[e]);
-        else st[kk * BPITCH + row] = h2d(v[e]);
+    for (int it = 0; it < HCH; ++it) {
+        const int idx = it * HT + tid;
+        *reinterpret_cast<h8*>(st + (idx / 8) * HP + (idx % 8) * 8) = r[it];
     }
+}
+
+// Element (row, k) of a stage, widened exactly to f64.
+template <int MODE>
+__device__ inline double hval(const uint16_t* __restrict__ st, int row, int k) {
+    return h2d(MODE == LOAD_MN ? st[k * HP + row] : st[row * HP + k]);
 }
 
 template <int AM, int BMD>
 __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
-    __shared__ double smem[2 * (A_STAGE + B_STAGE)];
-    double* As = smem;
-    double* Bs = smem + 2 * A_STAGE;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[4 * H_STAGE];
+    uint16_t* As = smem;
+    uint16_t* Bs = smem + 2 * H_STAGE;
     uint32_t plane, tm, tn;
     gemm_detail::decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
     const uint32_t m0 = tm * HGEMM_BM, n0 = tn * HGEMM_BN;
@@ -154,34 +156,34 @@ __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
 
-    h4 ra, rb;
+    h8 ra[HCH], rb[HCH];
     auto load = [&](uint32_t k0) {
         if (inner && k0 + HGEMM_BK <= p.k) {
-            ra = load4<AM, true, HGEMM_BM>(A, p.a_sm, p.a_sk, mrem, k0, p.k, tid);
-            rb = load4<BMD, true, HGEMM_BN>(B, p.b_sn, p.b_sk, nrem, k0, p.k, tid);
+            hload<AM, true>(ra, A, p.a_sm, p.a_sk, mrem, k0, p.k, tid);
+            hload<BMD, true>(rb, B, p.b_sn, p.b_sk, nrem, k0, p.k, tid);
         } else {
-            ra = load4<AM, false, HGEMM_BM>(A, p.a_sm, p.a_sk, mrem, k0, p.k, tid);
-            rb = load4<BMD, false, HGEMM_BN>(B, p.b_sn, p.b_sk, nrem, k0, p.k, tid);
+            hload<AM, false>(ra, A, p.a_sm, p.a_sk, mrem, k0, p.k, tid);
+            hload<BMD, false>(rb, B, p.b_sn, p.b_sk, nrem, k0, p.k, tid);
         }
     };
     const uint32_t ktiles = (p.k + HGEMM_BK - 1) / HGEMM_BK;
     load(0);
-    stage4<AM, true>(As, ra, tid);
-    stage4<BMD, false>(Bs, rb, tid);
+    hstage(As, ra, tid);
+    hstage(Bs, rb, tid);
     __syncthreads();
     for (uint32_t kt = 0; kt < ktiles; ++kt) {
         const int s = kt & 1;
         const bool more = kt + 1 < ktiles;
         if (more) load((kt + 1) * HGEMM_BK);
-        const double* as = As + s * A_STAGE;
-        const double* bs = Bs + s * B_STAGE;
-#pragma unroll
+        const uint16_t* as = As + s * H_STAGE;
+        const uint16_t* bs = Bs + s * H_STAGE;
+#pragma unroll 4
         for (int ks = 0; ks < HGEMM_BK / 4; ++ks) {
             double av[2], bv[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) av[i] = as[(wm * 32 + i * 16 + li) * APITCH + ks * 4 + lk];
+            for (int i = 0; i < 2; ++i) av[i] = hval<AM>(as, wm * 32 + i * 16 + li, ks * 4 + lk);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bv[j] = bs[(ks * 4 + lk) * BPITCH + wn * 32 + j * 16 + li];
+            for (int j = 0; j < 2; ++j) bv[j] = hval<BMD>(bs, wn * 32 + j * 16 + li, ks * 4 + lk);
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -189,8 +191,8 @@ __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
                     acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
         if (more) {
-            stage4<AM, true>(As + (s ^ 1) * A_STAGE, ra, tid);
-            stage4<BMD, false>(Bs + (s ^ 1) * B_STAGE, rb, tid);
+            hstage(As + (s ^ 1) * H_STAGE, ra, tid);
+            hstage(Bs + (s ^ 1) * H_STAGE, rb, tid);
         }
         __syncthreads();
     }

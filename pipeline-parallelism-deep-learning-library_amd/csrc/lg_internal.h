@@ -175,7 +175,7 @@ struct FillArgs {
 
 // f16 contraction (half operands as raw 16-bit patterns): products of halves are exact in
 // f64, sums run in f64 on the f64 matrix cores, and each output rounds once to f16.
-constexpr int HGEMM_BM = 64, HGEMM_BN = 64, HGEMM_BK = 16;
+constexpr int HGEMM_BM = 64, HGEMM_BN = 64, HGEMM_BK = 64;
 struct GemmHalfArgs {
     const uint16_t* a;
     const uint16_t* b;

@@ -383,8 +383,8 @@ def test_f16_plans_and_validation():
     p = C.plan_gemm(1.0, a, b, 0.0, c)
     assert (p["kind"], p["a_mode"], p["b_mode"], p["splits"]) == ("tiled", "k", "mn", 1)
     assert p["workgroups"] == 1
-    # 64-bit loads need 8-byte alignment and row strides in multiples of four halves.
-    p = C.plan_gemm(1.0, hv(Layout.dense([64, 46])), hv(Layout.transposed(46, 32)), 0.0, c)
+    # 128-bit loads need 16-byte alignment and row strides in multiples of eight halves.
+    p = C.plan_gemm(1.0, hv(Layout.dense([64, 44])), hv(Layout.transposed(44, 32)), 0.0, c)
     assert (p["a_mode"], p["b_mode"]) == ("strided", "strided")
     p = C.plan_gemm(1.0, hv(Layout.transposed(64, 48)), hv(Layout.transposed(48, 32)), 0.0, c)
     assert (p["a_mode"], p["b_mode"]) == ("mn", "k")

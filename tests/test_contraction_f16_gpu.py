@@ -108,8 +108,8 @@ def test_transposed_operands_are_read_in_place(ctx, pool, at, bt):
 
 def _mode_layout(operand, mode, rows, cols):
     """A [rows, cols] view of A (rows = M, cols = K) or B (rows = K, cols = N) whose plan
-    takes `mode`: "k" or "mn" unit stride along that axis with 8-byte alignment, "strided"
-    the same storage shifted by one element (misaligned for 64-bit loads)."""
+    takes `mode`: "k" or "mn" unit stride along that axis with 16-byte alignment, "strided"
+    the same storage shifted by one element (misaligned for 128-bit loads)."""
     contiguous_cols = (operand == "a") == (mode != "mn")
     lay = Layout.dense([rows, cols]) if contiguous_cols else Layout.transposed(rows, cols)
     if mode == "strided":
@@ -120,12 +120,12 @@ def _mode_layout(operand, mode, rows, cols):
 @pytest.mark.parametrize("amode", ["k", "mn", "strided"])
 @pytest.mark.parametrize("bmode", ["k", "mn", "strided"])
 def test_every_load_mode_pair_rounds_once(ctx, pool, amode, bmode):
-    """Each operand layout the tile kernel loads differently (64-bit loads along K, along M/N,
-    or predicated 16-bit loads) on a ragged 68x132x40 product. Halves on the 2^-10 grid keep
+    """Each operand layout the tile kernel loads differently (128-bit loads along K, along M/N,
+    or predicated 16-bit loads) on a ragged 72x136x40 product. Halves on the 2^-10 grid keep
     every partial sum exact in f64 (|sum| < 2^8 in steps of 2^-20), and alpha = -1/2,
     beta = 1/4 keep alpha*sum + beta*c exact, so numpy's correctly rounded f64 -> f16
     conversion of the f64 result is the exact value rounded once: bit for bit."""
-    m, n, k = 68, 132, 40
+    m, n, k = 72, 136, 40
     g = rng(11 + 3 * ["k", "mn", "strided"].index(amode) + ["k", "mn", "strided"].index(bmode))
     la, lb = _mode_layout("a", amode, m, k), _mode_layout("b", bmode, k, n)
     a = Half(pool, la, grid_halves(g, la.span()))
