@@ -110,6 +110,19 @@ __device__ inline void load_slice(floatx4 (&r)[G::LOADS], const float* __restric
     }
 }
 
+// The thread's first element of load i in a K-slice at k = 0 (LOAD_K and LOAD_MN): the slice
+// at k0 then starts k0 (LOAD_K) or k0*sk (LOAD_MN) elements later, one uniform offset, so an
+// interior slice costs one address add per load instead of a 64-bit multiply.
+template <int MODE, int BK, int R>
+__device__ inline const float* slice_ptr(const float* p, int64_t srow, int64_t sk, int i, int tid) {
+    const int idx = i * GEMM_THREADS + tid;
+    if constexpr (MODE == LOAD_MN) {
+        return p + static_cast<int64_t>(idx / (R / 4)) * sk + (idx % (R / 4)) * 4;
+    } else {
+        return p + static_cast<int64_t>(idx / (BK / 4)) * srow + (idx % (BK / 4)) * 4;
+    }
+}
+
 // Writes a loaded K-slice into its LDS stage. With SCALE (operand A) every element is first
 // multiplied by alpha, so each product the MFMAs form is (alpha*a)*b. alpha is finite here
 // (the planner sends non-finite alpha to the general kernel), so zero padding stays zero.
@@ -120,7 +133,9 @@ __device__ inline void store_slice(float* __restrict__ st, const floatx4 (&r)[G:
     for (int i = 0; i < Geo<BK, R>::LOADS; ++i) {
         const int idx = i * GEMM_THREADS + tid;
         floatx4 v = r[i];
-        if constexpr (SCALE) v = v * alpha;
+        if constexpr (SCALE) {
+            if (alpha != 1.0f) v = v * alpha;  // (1*a)*b is a*b: skip the multiply
+        }
         if constexpr (MODE == LOAD_MN) {
             const int kr = idx / (R / 4), row = (idx % (R / 4)) * 4;
             *reinterpret_cast<floatx4*>(st + kr * Geo<BK, R>::PR + row) = v;
@@ -206,10 +221,28 @@ void gemm_f32_mfma(GemmArgs p) {
     // Workgroup-uniform: the tile's M x N window lies inside the operands, so a K-slice is
     // "full" whenever its k range is.
     const bool inner = mrem >= TBM && nrem >= TBN;
+    const float* pa[GA::LOADS];
+    const float* pb[GB::LOADS];
+#pragma unroll
+    for (int i = 0; i < GA::LOADS; ++i) pa[i] = slice_ptr<AM, BK, TBM>(A, p.a_sm, p.a_sk, i, tid);
+#pragma unroll
+    for (int i = 0; i < GB::LOADS; ++i) pb[i] = slice_ptr<BMD, BK, TBN>(B, p.b_sn, p.b_sk, i, tid);
     auto load = [&](uint32_t k0) {
         if (inner && k0 + BK <= klen) {
-            load_slice<AM, true, BK, TBM>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
-            load_slice<BMD, true, BK, TBN>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
+            if constexpr (AM == LOAD_S) {
+                load_slice<AM, true, BK, TBM>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
+            } else {
+                const int64_t off = AM == LOAD_MN ? static_cast<int64_t>(k0) * p.a_sk : k0;
+#pragma unroll
+                for (int i = 0; i < GA::LOADS; ++i) ra[i] = *reinterpret_cast<const floatx4*>(pa[i] + off);
+            }
+            if constexpr (BMD == LOAD_S) {
+                load_slice<BMD, true, BK, TBN>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
+            } else {
+                const int64_t off = BMD == LOAD_MN ? static_cast<int64_t>(k0) * p.b_sk : k0;
+#pragma unroll
+                for (int i = 0; i < GB::LOADS; ++i) rb[i] = *reinterpret_cast<const floatx4*>(pb[i] + off);
+            }
         } else {
             load_slice<AM, false, BK, TBM>(ra, A, p.a_sm, p.a_sk, mrem, k0, klen, tid);
             load_slice<BMD, false, BK, TBN>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
