@@ -12,6 +12,8 @@ Functions (C implementations in oracle.c, each citing the reference code it rest
   contract_f64    tests/contraction_test.rs:200-268 (f64 accumulation, error magnitude)
   gate            tests/contraction_test.rs:280-313 accuracy gate
   north_star_tol  max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|
+  gemm_seq_16     CpuBackend::gemm on F16 / BF16 tensors: f32 accumulation, one 16-bit
+                  rounding per output (crates/cpu/src/lib.rs:270-291, 700-720)
   gelu, gelu_backward, add_bias, bias_grad, mse_grad, sgd_step, f32_to_bf16, bf16_to_f32
                   the CpuBackend activation and training ops (crates/cpu/src/lib.rs:297-533,
                   722-729, 809-842), sequential, one rounding per operation
@@ -278,6 +280,30 @@ def bf16_to_f32(h) -> np.ndarray:
 
 
 # ---- f16 contraction: the exact result rounded once ----------------------------------------
+def gemm_seq_16(kind: str, alpha: float, beta: float, a, b, c) -> np.ndarray:
+    """CpuBackend::gemm on F16 or BF16 tensors (crates/cpu/src/lib.rs:270-291 with
+    `accumulate`, :664-691): every element widened exactly to f32, acc = beta*C (0 when beta is
+    0, C unread), then acc += (alpha*a)*b over k in order in f32 unless alpha is 0, stored
+    rounded to the nearest 16-bit value, ties to even (`from_f32_const`, :700-720). a, b, c
+    are uint16 bit arrays [m, k], [k, n], [m, n]; returns the uint16 bits of C."""
+    def widen(h):
+        h = np.asarray(h, dtype=np.uint16)
+        if kind == "f16":
+            return h.view(np.float16).astype(np.float32)
+        return bf16_to_f32(h)
+    a32, b32 = widen(a), widen(b)
+    m, k = a32.shape
+    n = b32.shape[1]
+    acc = np.zeros((m, n), np.float32) if beta == 0.0 else np.float32(beta) * widen(c)
+    if alpha != 0.0:
+        al = np.float32(alpha)
+        for t in range(k):
+            acc = acc + (al * a32[:, t:t + 1]) * b32[t:t + 1, :]
+    if kind == "f16":
+        return acc.astype(np.float16).view(np.uint16)
+    return f32_to_bf16(acc).reshape(m, n)
+
+
 def f16_round_exact(x) -> int:
     """Bits of the f16 nearest the exact rational `x` (fractions.Fraction or int), ties to
     even, overflow to infinity, subnormals kept: the single rounding the reference's f16 path

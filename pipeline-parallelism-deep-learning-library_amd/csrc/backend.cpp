@@ -364,9 +364,6 @@ extern "C" lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_ten
                 require_range(b, k, n, size, "b");
             }
         }
-        if (a->dtype != LG_DTYPE_F32) {
-            core_fail(LG_CORE_UNSUPPORTED_DEVICE, "only f32 gemm runs on the HIP backend");
-        }
         if (ctx == nullptr) core_fail(LG_CORE_UNSUPPORTED_DEVICE, "null context");
         if (m == 0 || n == 0) {
             clear_last_error();
@@ -374,7 +371,7 @@ extern "C" lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_ten
         }
         const lg_status st = guarded([&] {
             enqueue_gemm_views(ctx, pick_stream(ctx, stream), alpha, to_view(a), to_view(b), beta,
-                               to_view(c));
+                               to_view(c), a->dtype);
         });
         if (st != LG_OK) return LG_CORE_UNSUPPORTED_DEVICE;  // launch failure; message kept
         return LG_CORE_OK;

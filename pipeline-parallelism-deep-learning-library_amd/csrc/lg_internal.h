@@ -183,6 +183,7 @@ struct GemmHalfArgs {
     int64_t a_sb, a_sm, a_sk, b_sb, b_sn, b_sk, c_sb, c_sm, c_sn;
     uint32_t m, n, k, batch, tiles_m, tiles_n;
     float alpha, beta;
+    uint32_t kind;  // 16-bit element type: 0 = f16, 1 = bf16
 };
 struct GeneralHalfArgs {
     const uint16_t* a;
@@ -191,6 +192,7 @@ struct GeneralHalfArgs {
     uint32_t m, n, k, batch;
     float alpha, beta;
     Axes4 a_batch, a_m, a_k, b_batch, b_n, b_k, c_batch, c_m, c_n;
+    uint32_t kind;
 };
 struct FillHalfArgs {
     uint16_t* c;
@@ -198,6 +200,7 @@ struct FillHalfArgs {
     uint32_t m, n, batch;
     float beta;
     Axes4 c_batch, c_m, c_n;
+    uint32_t kind;
 };
 void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int a_mode,
                       int b_mode);
@@ -285,9 +288,10 @@ namespace lg {
 void set_device(const lg_ctx* ctx);
 // Plans and enqueues the batched-matrix product C = alpha*A.B + beta*C on views whose ranges
 // the caller has already checked (the gemm form of the contraction planner; alias rules and
-// the scalar rules apply, views are not re-validated).
+// the scalar rules apply, views are not re-validated). dtype is an lg_dtype: F32 takes the
+// f32 kernels; F16 and BF16 the 16-bit ones (f64 sums of exact products, one rounding).
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
-                        float beta, const View& c);
+                        float beta, const View& c, uint32_t dtype);
 inline hipStream_t pick_stream(const lg_ctx* ctx, void* stream) {
     return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 }

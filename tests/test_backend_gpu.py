@@ -181,8 +181,7 @@ def test_errors_leave_c_unchanged_and_launch_nothing(hb):
         (a, alias, c, "Alias"),
         (shared, alias_ab, c, "Alias"),
         (a, a, c, "Alias"),
-        (hb.upload(B.DType.F16, [2, 2], bytes(8)), hb.upload(B.DType.F16, [2, 2], bytes(8)),
-         hb.upload(B.DType.F16, [2, 2], bytes(8)), "UnsupportedDevice"),
+        (hb.upload(B.DType.F16, [2, 2], bytes(8)), b, c, "Dtype"),
     ]
     launches = hb.debug_launches()
     for ta, tb, tc, kind in cases:
@@ -310,3 +309,112 @@ def test_non_finite_alpha_matches_the_sequential_loop(ctx, pool):
         assert np.array_equal(np.isnan(got), np.isnan(ref))
         fin = ~np.isnan(ref)
         assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+
+
+# ---- Backend::gemm on F16 / BF16 tensors (crates/cpu/src/lib.rs:270-291) --------------------
+from test_oracle import GEMM_16_KATS, to_16  # noqa: E402  (the reference's case list)
+
+DT16 = {"f16": B.DType.F16, "bf16": B.DType.BF16}
+
+
+def up16(hb, kind, bits16, shape, transpose=False):
+    """Upload uint16 bits as a [rows, cols] tensor; with `transpose`, as the transpose_matrix
+    view of the row-major [cols, rows] storage."""
+    bits16 = np.ascontiguousarray(np.asarray(bits16, np.uint16).reshape(shape))
+    if not transpose:
+        return hb.upload(DT16[kind], list(shape), bits16.tobytes())
+    t = hb.upload(DT16[kind], [shape[1], shape[0]], np.ascontiguousarray(bits16.T).tobytes())
+    return B.transpose_matrix(t)
+
+
+def down16(hb, t) -> np.ndarray:
+    return np.frombuffer(hb.download(t), dtype=np.uint16).copy()
+
+
+def widen16(kind, bits16) -> np.ndarray:
+    bits16 = np.asarray(bits16, np.uint16)
+    if kind == "f16":
+        return bits16.view(np.float16).astype(np.float64)
+    return oracle.bf16_to_f32(bits16).astype(np.float64)
+
+
+def ulp16(kind, x) -> np.ndarray:
+    """Spacing of the 16-bit type at |x| (its subnormal spacing below the normal range)."""
+    mant, emin, sub = (10, -14, 2.0 ** -24) if kind == "f16" else (7, -126, 2.0 ** -133)
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** emin)))
+    return np.maximum(2.0 ** (e - mant), sub)
+
+
+@pytest.mark.parametrize("case", GEMM_16_KATS)
+def test_16_bit_gemm_known_answers(hb, case):
+    kind, a, b, c, alpha, beta, want = case
+    k = len(a)
+    ta = up16(hb, kind, to_16(kind, a), (1, k))
+    tb = up16(hb, kind, to_16(kind, b), (k, 1))
+    tc = up16(hb, kind, to_16(kind, c), (1, 1))
+    n0 = len(hb.debug_launches())
+    hb.gemm(ta, tb, tc, alpha, beta)
+    assert int(down16(hb, tc)[0]) == want
+    assert len(hb.debug_launches()) == n0 + 1
+
+
+def test_16_bit_gemm_reads_no_operand_when_alpha_is_zero(hb):
+    nan = np.array([0x7E00], np.uint16)
+    two = to_16("f16", [2.0])
+    tc = up16(hb, "f16", two, (1, 1))
+    hb.gemm(up16(hb, "f16", nan, (1, 1)), up16(hb, "f16", nan, (1, 1)), tc, 0.0, 1.0)
+    assert int(down16(hb, tc)[0]) == int(two[0])
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("layout", ["rm", "at", "bt"])
+def test_16_bit_gemm_rounds_exact_sums_once(hb, kind, layout):
+    """Inputs on a grid the 16-bit type holds exactly with |sum| < 2^9 in steps of 2^-14 (exact
+    in f32 and f64): the stored value is the exact sum rounded once, as the reference's f32
+    accumulation also gives there, bit for bit, in all three layouts and over ragged tiles."""
+    m, k, n = 75, 70, 131
+    g = rng(hash((kind, layout)) % 1000)
+    step = 2.0 ** -7
+    av = (g.integers(-256, 256, (m, k)) * step).astype(np.float32)
+    bv = (g.integers(-256, 256, (k, n)) * step).astype(np.float32)
+    cv = (g.integers(-256, 256, (m, n)) * step).astype(np.float32)
+    a16, b16, c16 = to_16(kind, av.ravel()), to_16(kind, bv.ravel()), to_16(kind, cv.ravel())
+    ta = up16(hb, kind, a16, (m, k), transpose=layout == "at")
+    tb = up16(hb, kind, b16, (k, n), transpose=layout == "bt")
+    tc = up16(hb, kind, c16, (m, n))
+    hb.gemm(ta, tb, tc, -0.5, 0.25)
+    exact = -0.5 * (av.astype(np.float64) @ bv.astype(np.float64)) + 0.25 * cv.astype(np.float64)
+    e32 = exact.astype(np.float32).ravel()
+    assert np.array_equal(e32.astype(np.float64), exact.ravel())  # exact in f32, so one rounding:
+    want = e32.astype(np.float16).view(np.uint16) if kind == "f16" else oracle.f32_to_bf16(e32)
+    assert np.array_equal(down16(hb, tc), want)
+    cpu = oracle.gemm_seq_16(kind, -0.5, 0.25, a16.reshape(m, k), b16.reshape(k, n),
+                             c16.reshape(m, n))
+    assert np.array_equal(cpu.ravel(), want)
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("m,k,n,alpha,beta", [(64, 64, 64, 1.0, 0.0), (130, 300, 70, 0.75, -0.5),
+                                              (256, 512, 192, 1.0, 1.0), (3, 1000, 5, -2.0, 0.0)])
+def test_16_bit_gemm_against_the_cpu_restatement(hb, kind, m, k, n, alpha, beta):
+    """Random data: the result is the 16-bit rounding of an f64 sum of exact products, so it
+    is within half a 16-bit ulp (plus the f64 sum's error) of the exact value, and within one
+    16-bit ulp plus the f32 accumulation bound of the reference's f32-accumulated result."""
+    g = rng(m * 31 + k * 7 + n + (kind == "bf16"))
+
+    def rand16(count):
+        x = g.uniform(-1, 1, count).astype(np.float32)
+        return x.astype(np.float16).view(np.uint16) if kind == "f16" else oracle.f32_to_bf16(x)
+    a16, b16, c16 = rand16(m * k), rand16(k * n), rand16(m * n)
+    tc = up16(hb, kind, c16, (m, n))
+    hb.gemm(up16(hb, kind, a16, (m, k)), up16(hb, kind, b16, (k, n)), tc, alpha, beta)
+    got = widen16(kind, down16(hb, tc)).reshape(m, n)
+    a64, b64, c64 = (widen16(kind, x) for x in (a16, b16, c16))
+    a64, b64, c64 = a64.reshape(m, k), b64.reshape(k, n), c64.reshape(m, n)
+    exact = alpha * (a64 @ b64) + (beta * c64 if beta != 0.0 else 0.0)
+    mag = np.abs(alpha) * (np.abs(a64) @ np.abs(b64)) + np.abs(beta * c64)
+    spacing = ulp16(kind, np.maximum(np.abs(exact), np.abs(got)))
+    assert np.all(np.abs(got - exact) <= 0.5 * spacing + (k + 2) * 2.0 ** -52 * mag)
+    cpu = widen16(kind, oracle.gemm_seq_16(kind, alpha, beta, a16.reshape(m, k),
+                                           b16.reshape(k, n), c16.reshape(m, n))).reshape(m, n)
+    assert np.all(np.abs(got - cpu) <= ulp16(kind, cpu) + (k + 2) * 2.0 ** -24 * mag)

@@ -362,3 +362,53 @@ def test_contract_exact_f16_small_closed_forms():
     assert oracle.contract_exact_f16(1.0, a, b, 0.0, np.zeros((1, 1), np.float16)).view(np.float16)[0, 0] == 2048
     a = np.array([[2048, 3]], np.float16)
     assert oracle.contract_exact_f16(1.0, a, b, 0.0, np.zeros((1, 1), np.float16)).view(np.float16)[0, 0] == 2052
+
+
+# ---- CpuBackend::gemm on F16 / BF16 (crates/cpu/src/invariants.rs:556-720) ------------------
+TIE_DOWN = 1.0 / 256.0          # the exact halfway step at 1.0 for bf16 (ulp 2^-7)
+ONE_PLUS_ULP = 1.0 + 1.0 / 128.0
+GEMM_16_KATS = [  # (dtype, a, b, c, alpha, beta, expected bits), the reference's case list
+    ("f16", [2048.0, 1.0], [1.0, 1.0], [0.0], 1.0, 0.0, 0x6800),
+    ("f16", [2050.0, 1.0], [1.0, 1.0], [0.0], 1.0, 0.0, 0x6802),
+    ("f16", [2048.0, 1.0, 1.0], [1.0, 1.0, 1.0], [0.0], 1.0, 0.0, 0x6801),
+    ("f16", [2048.0, 1.0, 0.5], [1.0, 1.0, 1.0], [0.0], 1.0, 0.0, 0x6801),
+    ("f16", [-2048.0, -1.0], [1.0, 1.0], [0.0], 1.0, 0.0, 0xE800),
+    ("f16", [2048.0, 1.0], [1.0, 1.0], [1.0], 1.0, 1.0, 0x6801),
+    ("bf16", [1.0, TIE_DOWN], [1.0, 1.0], [0.0], 1.0, 0.0, 0x3F80),
+    ("bf16", [ONE_PLUS_ULP, TIE_DOWN], [1.0, 1.0], [0.0], 1.0, 0.0, 0x3F82),
+    ("bf16", [1.0, TIE_DOWN, TIE_DOWN], [1.0, 1.0, 1.0], [0.0], 1.0, 0.0, 0x3F81),
+    ("bf16", [-1.0, -TIE_DOWN], [1.0, 1.0], [0.0], 1.0, 0.0, 0xBF80),
+    ("bf16", [1.0, TIE_DOWN], [1.0, 1.0], [TIE_DOWN], 1.0, 1.0, 0x3F81),
+]
+
+
+def to_16(kind, values):
+    v = np.asarray(values, np.float32)
+    bits = v.astype(np.float16).view(np.uint16) if kind == "f16" else oracle.f32_to_bf16(v)
+    back = (bits.view(np.float16).astype(np.float32) if kind == "f16" else oracle.bf16_to_f32(bits))
+    assert np.array_equal(back, v), "fixture value not exact in the 16-bit type"
+    return bits
+
+
+@pytest.mark.parametrize("case", GEMM_16_KATS)
+def test_gemm_seq_16_on_the_reference_known_answers(case):
+    kind, a, b, c, alpha, beta, want = case
+    k = len(a)
+    got = oracle.gemm_seq_16(kind, alpha, beta, to_16(kind, a).reshape(1, k),
+                             to_16(kind, b).reshape(k, 1), to_16(kind, c).reshape(1, 1))
+    assert int(got[0, 0]) == want
+
+
+def test_gemm_seq_16_reads_nothing_unread_and_sums_in_f32():
+    nan = np.array([[0x7E00]], np.uint16)
+    two = to_16("f16", [2.0]).reshape(1, 1)
+    assert int(oracle.gemm_seq_16("f16", 0.0, 1.0, nan, nan, two)[0, 0]) == int(two[0, 0])
+    # f32 accumulation, not f16: 2048 + 1 + 1 in f16 steps would stay at 2048.
+    ones = to_16("f16", [2048.0, 1.0, 1.0]).reshape(1, 3)
+    assert int(oracle.gemm_seq_16("f16", 1.0, 0.0, ones, to_16("f16", [1.0] * 3).reshape(3, 1),
+                                  nan)[0, 0]) == 0x6801
+    # and f32, not f64: 1 + 2^-8 + 2^-30 is just above the bf16 tie at 1 + 2^-8 (0x3F81),
+    # but its f32 sum drops the 2^-30 and lands on the tie, which rounds to even: 0x3F80.
+    ops = to_16("bf16", [1.0, 2.0 ** -8, 2.0 ** -30]).reshape(1, 3)
+    got = oracle.gemm_seq_16("bf16", 1.0, 0.0, ops, to_16("bf16", [1.0] * 3).reshape(3, 1), nan)
+    assert int(got[0, 0]) == 0x3F80
