@@ -308,6 +308,18 @@ lg_core_error lg_backend_sgd_step(lg_ctx* ctx, void* stream, const lg_tensor* w,
 lg_core_error lg_backend_convert(lg_ctx* ctx, void* stream, const lg_tensor* x,
                                  const lg_tensor* y);
 
+/* Backend::download_into and Backend::upload_into (crates/core/src/lib.rs:118-133, as
+ * CpuBackend checks them at crates/cpu/src/lib.rs:328-370): a tensor's row-major bytes into
+ * caller memory, or caller bytes over every element of an existing tensor, allocating
+ * nothing. Checks in order: decodable tensor, byte count equal to the tensor's (else Shape),
+ * row-major at offset 0 (else UnsupportedLayout), storage holding the bytes (else Shape).
+ * Both copy on `stream` (NULL = context stream) after every earlier call there and return
+ * when the copy is done: `out` holds the bytes, and `bytes` may be reused. */
+lg_core_error lg_backend_download_into(lg_ctx* ctx, void* stream, const lg_tensor* t,
+                                       uint8_t* out, uint64_t out_len);
+lg_core_error lg_backend_upload_into(lg_ctx* ctx, void* stream, const uint8_t* bytes,
+                                     uint64_t len, const lg_tensor* t);
+
 /* ---------------------------------------------------------------------------------------
  * Wire format of stage boundaries (crates/core/src/lib.rs:298-412)
  *

@@ -306,6 +306,41 @@ lg_core_error lg_backend_mse_grad(lg_ctx* ctx, void* stream, const lg_tensor* y,
     });
 }
 
+lg_core_error lg_backend_download_into(lg_ctx* ctx, void* stream, const lg_tensor* t,
+                                       uint8_t* out, uint64_t out_len) {
+    return run_op([&] {
+        decode({t});
+        const uint64_t len = nbytes(t);
+        if (out_len != len) core_fail(LG_CORE_SHAPE, "output length differs from the tensor's bytes");
+        if (!packed_layout(t)) core_fail(LG_CORE_UNSUPPORTED_LAYOUT, "tensor is not row-major at offset 0");
+        if (len > t->bytes) core_fail(LG_CORE_SHAPE, "tensor reaches past its storage");
+        if (len != 0 && out == nullptr) core_fail(LG_CORE_SHAPE, "null output");
+        hipStream_t s = device_stream(ctx, stream);
+        // After every earlier call on the stream; `out` holds the bytes when this returns.
+        if (len) check_hip(hipMemcpyAsync(out, t->base, len, hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    });
+}
+
+lg_core_error lg_backend_upload_into(lg_ctx* ctx, void* stream, const uint8_t* bytes,
+                                     uint64_t len, const lg_tensor* t) {
+    return run_op([&] {
+        decode({t});
+        const uint64_t need = nbytes(t);
+        if (len != need) core_fail(LG_CORE_SHAPE, "byte count differs from the tensor's bytes");
+        if (!packed_layout(t)) core_fail(LG_CORE_UNSUPPORTED_LAYOUT, "tensor is not row-major at offset 0");
+        if (need > t->bytes) core_fail(LG_CORE_SHAPE, "tensor reaches past its storage");
+        if (need != 0 && bytes == nullptr) core_fail(LG_CORE_SHAPE, "null bytes");
+        hipStream_t s = device_stream(ctx, stream);
+        // Ordered after every earlier call and before every later one on the stream; `bytes`
+        // may be reused as soon as this returns.
+        if (need) {
+            check_hip(hipMemcpyAsync(t->base, bytes, need, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+        }
+        check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+    });
+}
+
 lg_core_error lg_backend_sgd_step(lg_ctx* ctx, void* stream, const lg_tensor* w,
                                   const lg_tensor* dw, float lr) {
     return run_op([&] {

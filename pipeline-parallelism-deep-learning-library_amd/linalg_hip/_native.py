@@ -93,6 +93,8 @@ SIGNATURES = {
     "lg_backend_mse_grad": (i32, [vp, vp, TP, TP, TP, ctypes.POINTER(F)]),
     "lg_backend_sgd_step": (i32, [vp, vp, TP, TP, F]),
     "lg_backend_convert": (i32, [vp, vp, TP, TP]),
+    "lg_backend_download_into": (i32, [vp, vp, TP, vp, u64]),
+    "lg_backend_upload_into": (i32, [vp, vp, vp, u64, TP]),
     "lg_wire_write_header": (i32, [u32, ctypes.POINTER(u64), u32, vp, ctypes.POINTER(u64)]),
     "lg_wire_parse_header": (i32, [vp, u64, ctypes.POINTER(u32), ctypes.POINTER(u64),
                                    ctypes.POINTER(u32), ctypes.POINTER(u64)]),

@@ -187,6 +187,24 @@ class HipBackend:
     def download_f32(self, t: Tensor) -> np.ndarray:
         return np.frombuffer(self.download(t), dtype=np.float32).copy()
 
+    def download_into(self, t: Tensor, out) -> None:
+        """`Backend::download_into` (crates/cpu/src/lib.rs:328-346): the tensor's row-major
+        bytes into `out` (a writable buffer: bytearray or contiguous numpy array), no host
+        allocation; returns after every earlier call has completed."""
+        view = memoryview(out).cast("B")
+        if view.readonly:
+            raise BackendError("Shape", "output buffer is read-only")
+        buf = (ctypes.c_uint8 * len(view)).from_buffer(view) if len(view) else None
+        _raise(N.lib().lg_backend_download_into(self.ctx.handle, None, ctypes.byref(t.to_c()),
+                                                buf, len(view)))
+
+    def upload_into(self, data, t: Tensor) -> None:
+        """`Backend::upload_into` (crates/cpu/src/lib.rs:348-370): overwrites every element of
+        the existing row-major tensor with `data`'s bytes; `data` may be reused at once."""
+        raw = bytes(memoryview(data).cast("B"))
+        _raise(N.lib().lg_backend_upload_into(self.ctx.handle, None, raw, len(raw),
+                                              ctypes.byref(t.to_c())))
+
     def gemm(self, a: Tensor, b: Tensor, c: Tensor, alpha: float, beta: float) -> None:
         """`Backend::gemm` (crates/core/src/lib.rs:143-164); raises `BackendError`."""
         _raise(N.lib().lg_backend_gemm(self.ctx.handle, None, ctypes.byref(a.to_c()),

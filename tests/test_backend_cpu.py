@@ -259,3 +259,41 @@ def test_training_ops_pass_their_checks_on_valid_operands():
         with pytest.raises(B.BackendError, match="null context") as e:
             B.op_checks(op, *args)
         assert e.value.kind == "UnsupportedDevice", op
+
+
+def transfer_kind(direction: str, t: B.Tensor, length: int) -> str:
+    """lg_backend_download_into / upload_into with no context: the first failing check, or
+    UnsupportedDevice ("null context") when every check passes."""
+    import ctypes
+    from linalg_hip import _native as N
+    buf = (ctypes.c_uint8 * max(length, 1))()
+    if direction == "down":
+        code = N.lib().lg_backend_download_into(None, None, ctypes.byref(t.to_c()), buf, length)
+    else:
+        code = N.lib().lg_backend_upload_into(None, None, buf, length, ctypes.byref(t.to_c()))
+    with pytest.raises(B.BackendError) as e:
+        B._raise(code)
+    return e.value.kind
+
+
+@pytest.mark.parametrize("direction", ["down", "up"])
+def test_transfer_into_checks_in_the_reference_order(direction):
+    """download_into / upload_into (crates/cpu/src/lib.rs:328-370): byte count first (Shape),
+    then row-major at offset 0 (UnsupportedLayout), then the storage (Shape)."""
+    t = rm([3, 5])
+    assert transfer_kind(direction, t, 60) == "UnsupportedDevice"
+    assert transfer_kind(direction, t, 59) == "Shape"
+    assert transfer_kind(direction, t, 61) == "Shape"
+    # A wrong length is reported before a wrong layout.
+    assert transfer_kind(direction, transposed(3, 5), 59) == "Shape"
+    assert transfer_kind(direction, transposed(3, 5), 60) == "UnsupportedLayout"
+    shifted = B.Tensor(storage(64), B.DType.F32, [3, 5], [5, 1], 1)
+    assert transfer_kind(direction, shifted, 60) == "UnsupportedLayout"
+    short = B.Tensor(storage(56), B.DType.F32, [3, 5], [5, 1])
+    assert transfer_kind(direction, short, 60) == "Shape"
+    half = rm([4], B.DType.BF16)
+    assert transfer_kind(direction, half, 8) == "UnsupportedDevice"
+    odd = rm([2])
+    odd.dtype = 9
+    assert transfer_kind(direction, odd, 8) == "Wire"
+    assert transfer_kind(direction, rm([0, 3]), 0) == "UnsupportedDevice"

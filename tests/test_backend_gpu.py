@@ -418,3 +418,48 @@ def test_16_bit_gemm_against_the_cpu_restatement(hb, kind, m, k, n, alpha, beta)
     cpu = widen16(kind, oracle.gemm_seq_16(kind, alpha, beta, a16.reshape(m, k),
                                            b16.reshape(k, n), c16.reshape(m, n))).reshape(m, n)
     assert np.all(np.abs(got - cpu) <= ulp16(kind, cpu) + (k + 2) * 2.0 ** -24 * mag)
+
+
+def test_download_into_and_upload_into(hb):
+    """Backend::download_into / upload_into (crates/core/src/lib.rs:118-133): row-major bytes
+    out into caller memory and back over an existing tensor, in call order; a failed check
+    changes nothing."""
+    x = hb.upload_f32([3, 5], np.arange(15, dtype=np.float32))
+    out = np.zeros(15, np.float32)
+    hb.download_into(x, out)
+    assert np.array_equal(out, np.arange(15, dtype=np.float32))
+    # In order with earlier work: the gelu enqueued before is in the bytes.
+    y = hb.alloc(B.DType.F32, [3, 5])
+    hb.gelu(x, y)
+    got = bytearray(60)
+    hb.download_into(y, got)
+    assert np.array_equal(np.frombuffer(bytes(got), np.float32), hb.download_f32(y))
+    # upload_into overwrites every element; the source may be reused right away.
+    src = np.linspace(-1, 1, 15, dtype=np.float32)
+    hb.upload_into(src, y)
+    src[:] = 7.0
+    assert np.array_equal(hb.download_f32(y), np.linspace(-1, 1, 15, dtype=np.float32))
+    # bf16 bytes travel unchanged.
+    h = hb.alloc(B.DType.BF16, [4])
+    hb.upload_into(np.array([0x3F80, 0xBF81, 0x7FC0, 0x0001], np.uint16), h)
+    back = np.zeros(4, np.uint16)
+    hb.download_into(h, back)
+    assert back.tolist() == [0x3F80, 0xBF81, 0x7FC0, 0x0001]
+    # Failed checks: nothing written either way.
+    before = hb.download_f32(y)
+    for bad, kind in [(np.zeros(14, np.float32), "Shape"), (np.zeros(16, np.float32), "Shape")]:
+        with pytest.raises(B.BackendError) as e:
+            hb.upload_into(bad, y)
+        assert e.value.kind == kind
+        sentinel = np.full(bad.size, 3.0, np.float32)
+        with pytest.raises(B.BackendError) as e:
+            hb.download_into(y, sentinel)
+        assert e.value.kind == kind and np.all(sentinel == 3.0)
+    with pytest.raises(B.BackendError) as e:
+        hb.upload_into(np.zeros(15, np.float32), B.transpose_matrix(y))
+    assert e.value.kind == "UnsupportedLayout"
+    assert np.array_equal(hb.download_f32(y), before)
+    # Zero elements: nothing to move.
+    z = hb.alloc(B.DType.F32, [0, 4])
+    hb.download_into(z, bytearray())
+    hb.upload_into(b"", z)
