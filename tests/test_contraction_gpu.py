@@ -380,6 +380,48 @@ def test_split_partials_shared_across_streams():
         ctx2.close()
 
 
+def test_split_partials_under_concurrent_threads(ctx, pool):
+    """Four host threads, each with its own stream on one context, enqueue split-K GEMMs of
+    different sizes in a loop with no host waits between calls; the shared partial buffer is
+    handed out under the context's lock and ordered across streams, so every result matches
+    the single-threaded one bit for bit."""
+    import threading
+    shapes = [(8, 8, 65536), (40, 24, 30000), (130, 200, 20000), (64, 64, 50000)]
+    jobs = []
+    for i, (m, n, k) in enumerate(shapes):
+        g = rng(2200 + i)
+        a = Tensor.random(pool, Layout.dense([m, k]), g)
+        b = Tensor.random(pool, Layout.dense([k, n]), g)
+        ref = Tensor(pool, Layout.dense([m, n]))
+        assert C.plan_gemm(1.0, a.view(), b.view(), 0.0, ref.view())["kind"] == "split"
+        C.gemm(ctx, 1.0, a.view(), b.view(), 0.0, ref.view())
+        outs = [Tensor(pool, Layout.dense([m, n])) for _ in range(6)]
+        jobs.append((a, b, ref.read(), outs))
+    errors = []
+
+    def worker(job):
+        a, b, _, outs = job
+        s = ctx.new_stream()
+        try:
+            for c in outs:
+                C.encode_gemm(ctx, s, 1.0, a.view(), b.view(), 0.0, c.view())
+            s.wait_until_completed()
+        except BaseException as e:  # reported below
+            errors.append(e)
+        finally:
+            s.close()
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors and not any(t.is_alive() for t in threads)
+    for _, _, want, outs in jobs:
+        for c in outs:
+            assert np.array_equal(c.read().view(np.uint32), want.view(np.uint32))
+
+
 # --------------------------------------------------------------------------------------
 # Random einsum sweep (tests/contraction_test.rs:1008-1096), own seeded generator.
 # --------------------------------------------------------------------------------------
