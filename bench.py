@@ -162,7 +162,7 @@ def bench_gemm(ctx, events, pool, L, C, name, m, n, k, args, a_t=False, b_t=Fals
             "host_ms": HOST_MS[launch], "tflops": tflops,
             "frac": tflops / PEAK_TFLOPS,
             "plan": {k_: plan[k_] for k_ in ("kind", "a_mode", "b_mode", "splits", "workgroups")},
-            "_host": (a, b)}
+            "_host": (a, b), "_geom": (m, n, k, a_t, b_t, batch, beta)}
 
 
 def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
@@ -182,7 +182,7 @@ def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
     return {"name": name, "ms": ms, "ms_median": med, "ms_best": best,
             "host_ms": HOST_MS[launch], "gbs": gbs, "frac": gbs / PEAK_GBS,
             "plan": {k_: plan[k_] for k_ in ("kind", "vector", "workgroups", "shape")},
-            "_host": x}
+            "_host": x, "_geom": (list(shape), list(perm))}
 
 
 def bench_copy(ctx, events, pool, L, P, n, args):
@@ -321,47 +321,99 @@ def traffic_from_profile(name):
         return None
 
 
-def cpu_baselines(gemm_host, perm_host, args):
-    """crates/cpu restated (oracle/), timed on bounded samples of the same workloads."""
+# Bounded CPU samples per GEMM workload: (literal rows, rows for the threaded variant or None
+# for all, batches for the threaded variant). About 20 s of CPU work for the whole set.
+CPU_GEMM_SAMPLES = {"gemm4096": (48, None, 1), "c1": (512, None, 1), "c3": (32, None, 4),
+                    "c4": (4, None, 1), "c5": (4, 256, 1)}
+
+
+def cpu_gemm_rates(host, geom, seq_rows, fast_rows, fast_batches, threads):
+    """crates/cpu's gemm restated (oracle/): the literal single-thread k-order loop on the
+    first `seq_rows` output rows, and the bit-identical loop-interchanged variant on `threads`
+    threads, on the workload's own host inputs; FLOP and seconds of each sample."""
     import oracle
-    out = {}
-    a, b = gemm_host
-    n = 4096
-    # Literal single-thread accumulation (what crates/cpu runs): a sample of output rows.
-    rows = np.arange(48, dtype=np.uint64)
-    c = np.zeros(n * n, np.float32)
+    a, b = host
+    m, n, k, a_t, b_t, batch, beta = geom
+    seq_rows, fast_batches = min(seq_rows, m), min(fast_batches, batch)
+    fast_rows = None if fast_rows is None or fast_rows >= m else fast_rows
+    a_st = (1, m) if a_t else (k, 1)
+    b_st = (1, k) if b_t else (n, 1)
+    c = np.zeros(m * n, np.float32)
     t0 = time.perf_counter()
-    for r in rows:
-        oracle.gemm_seq(1, n, n, 1.0, 0.0, a, int(r) * n, (n, 1), b, 0, (n, 1), c, int(r) * n, (n, 1))
-    dt = time.perf_counter() - t0
-    flops = 2.0 * len(rows) * n * n
-    out["gemm_seq"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-                       "sample": f"{len(rows)} of 4096 output rows of the 4096^3 gemm, "
-                                 f"literal k-order loop ({dt:.1f} s)"}
-    threads = min(os.cpu_count() or 1, 16)
-    rows = np.arange(n, dtype=np.uint64)
+    for r in range(seq_rows):
+        oracle.gemm_seq(1, n, k, 1.0, beta, a, r * a_st[0], a_st, b, 0, b_st, c, r * n, (n, 1))
+    seq = (2.0 * seq_rows * n * k, time.perf_counter() - t0)
+    rows = None if fast_rows is None else np.arange(fast_rows, dtype=np.uint64)
+    nr = (m if fast_rows is None else fast_rows) * fast_batches
     t0 = time.perf_counter()
-    oracle.gemm_fast(n, n, n, 1.0, 0.0, a, 0, (n, 1), b, 0, (n, 1), c, 0, (n, 1), rows=rows,
-                     threads=threads)
-    dt = time.perf_counter() - t0
-    flops = 2.0 * len(rows) * n * n
-    out["gemm_fast"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads,
-                        "kind": "port",
-                         "sample": f"all {len(rows)} output rows of the 4096^3 gemm, bit-identical "
-                                  f"loop-interchanged variant on {threads} threads ({dt:.1f} s)"}
-    x = perm_host
-    shape, perm = [512, 1024, 256], [2, 0, 1]
-    # gather_words over all 256 output planes (dst[c] = src[:, :, c]).
-    sample_planes = 256
-    t0 = time.perf_counter()
+    for bi in range(fast_batches):
+        oracle.gemm_fast(m, n, k, 1.0, beta, a, bi * m * k, a_st, b, bi * k * n, b_st, c, 0,
+                         (n, 1), rows=rows, threads=threads)
+    fast = (2.0 * nr * n * k, time.perf_counter() - t0)
+    return seq, fast, (seq_rows, nr, batch * m)
+
+
+def cpu_perm_rates(x, geom, threads):
+    """gather_words restated (oracle/) over the whole permuted view, one thread and
+    `threads` threads: bytes moved (one read + one write per word) and seconds."""
+    import oracle
+    shape, perm = geom
     words = x.view(np.uint32)
-    oracle.gather_words(words, 1, 0, [sample_planes, 512, 1024], [1, 1024 * 256, 256])
-    dt = time.perf_counter() - t0
-    nbytes = 2.0 * sample_planes * 512 * 1024 * 4
-    out["permute"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                      "sample": f"gather_words of all {sample_planes} output planes of "
-                                f"[512,1024,256] perm (2,0,1), 1 GiB moved ({dt:.1f} s)"}
-    return out
+    st = [int(np.prod(shape[d + 1:], dtype=np.int64)) for d in range(len(shape))]
+    pshape, pst = [shape[p] for p in perm], [st[p] for p in perm]
+    nbytes = 2.0 * words.size * 4
+    t0 = time.perf_counter()
+    oracle.gather_words(words, 1, 0, pshape, pst)
+    one = (nbytes, time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    oracle.gather_words_mt(words, 1, 0, pshape, pst, threads=threads)
+    par = (nbytes, time.perf_counter() - t0)
+    return one, par
+
+
+def attach_cpu_baselines(results, threads):
+    """Adds cpu_baseline (one core, the literal restatement) and cpu_baseline_parallel
+    (`threads` cores, bit-identical) to every GEMM and permutation workload, timed on bounded
+    samples of the workload's own inputs after all GPU timing is done."""
+    def tf(work, what, cores):
+        flop, dt = work
+        return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+                "sample": f"{what} ({dt:.2f} s)"}
+
+    def gb(work, what, cores):
+        nbytes, dt = work
+        return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+                "sample": f"{what} ({dt:.2f} s)"}
+
+    for name, r in results.items():
+        if not isinstance(r, dict):
+            continue
+        parts = r.get("parts") or [r]
+        if all("_geom" in p and isinstance(p["_host"], tuple) for p in parts):
+            spec = CPU_GEMM_SAMPLES.get(name)
+            if spec is None:
+                continue
+            tot = [[0.0, 0.0], [0.0, 0.0]]
+            for p in parts:
+                seq, fast, (sr, fr, total_rows) = cpu_gemm_rates(p.pop("_host"), p.pop("_geom"),
+                                                                 *spec, threads)
+                p["cpu_baseline"] = tf(seq, f"{sr} of {total_rows} output rows, literal "
+                                            "k-order loop", 1)
+                p["cpu_baseline_parallel"] = tf(fast, f"{fr} of {total_rows} output rows, "
+                                                      "bit-identical loop-interchanged variant "
+                                                      f"on {threads} threads", threads)
+                for i, w in enumerate((seq, fast)):
+                    tot[i][0] += w[0]
+                    tot[i][1] += w[1]
+            if len(parts) > 1:
+                r["cpu_baseline"] = tf(tot[0], "the three products' literal samples", 1)
+                r["cpu_baseline_parallel"] = tf(tot[1], "the three products' threaded samples",
+                                                threads)
+        elif "_geom" in r:
+            one, par = cpu_perm_rates(r.pop("_host"), r.pop("_geom"), threads)
+            r["cpu_baseline"] = gb(one, "gather_words over the whole permuted view", 1)
+            r["cpu_baseline_parallel"] = gb(par, "gather_words_mt over the whole permuted view, "
+                                                 f"{threads} contiguous output ranges", threads)
 
 
 def main() -> int:
@@ -431,8 +483,6 @@ def main() -> int:
                         seed=(9, 11), sigma=0.02, beta=1.0)
         ms = y["ms"] + dx["ms"] + dw["ms"]
         tf = 3 * 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        for r in (y, dx, dw):
-            r.pop("_host")
         return {"name": "C5 linear-layer step (3 gemms)", "ms": ms, "tflops": tf,
                 "frac": tf / PEAK_TFLOPS, "parts": [y, dx, dw]}
     run("c5", c5)
@@ -448,6 +498,7 @@ def main() -> int:
         r = bench_perm(ctx, events, pool, L, P, "transpose [8191,4099] perm (1,0)", [8191, 4099],
                        [1, 0], 3000, args)
         r.pop("_host")
+        r.pop("_geom")
         r["copy_gbs"] = bench_copy(ctx, events, pool, L, P, 8191 * 4099, args)
         r["ratio_vs_copy"] = r["gbs"] / r["copy_gbs"]
         return r
@@ -456,15 +507,13 @@ def main() -> int:
     run("f16", lambda: bench_gemm_f16(ctx, events, pool, L, C, 4096, 4096, 4096, args))
 
     train = results.pop("train", None)
-    gemm_host = results.get("gemm4096", {}).pop("_host", None)
-    perm_host = results.get("c2b", {}).pop("_host", None)
+    if not args.no_cpu:
+        print("[bench] cpu baselines ...", file=sys.stderr, flush=True)
+        attach_cpu_baselines(results, min(os.cpu_count() or 1, 16))
     for r in results.values():
-        if isinstance(r, dict):
-            r.pop("_host", None)
-
-    cpu = None
-    if not args.no_cpu and gemm_host is not None and perm_host is not None:
-        cpu = cpu_baselines(gemm_host, perm_host, args)
+        for p in ([r] + list(r.get("parts", []))) if isinstance(r, dict) else []:
+            p.pop("_host", None)
+            p.pop("_geom", None)
 
     head = results.get("gemm4096")
     perm = results.get("c2b")
@@ -483,9 +532,9 @@ def main() -> int:
                             "kernel": "gemm_f32_mfma<0, 1, 16, 2, 2> (A K-contiguous, B N-contiguous, 128x128 tile)",
                             "profile": "profiles/gemm_f32_mfma_gemm4096.md, profiles/traffic_gemm4096.txt",
                             "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
-    if cpu:
-        line["cpu_baseline"] = cpu["gemm_seq"]
-        line["cpu_baseline_parallel"] = cpu["gemm_fast"]
+    if head and "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
+        line["cpu_baseline_parallel"] = head["cpu_baseline_parallel"]
     if perm:
         line["permute"] = {"value": round(perm["gbs"], 1), "unit": "GB/s",
                            "workload": perm["name"], "ms_per_step": round(perm["ms"], 4),
@@ -496,7 +545,8 @@ def main() -> int:
                                         "kernel": "perm_tile<1, false, true, 128, 64, 3, 256> (non-temporal loads and stores)",
                                         "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
                                         "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
-                           "cpu_baseline": cpu["permute"] if cpu else None}
+                           "cpu_baseline": perm.get("cpu_baseline"),
+                           "cpu_baseline_parallel": perm.get("cpu_baseline_parallel")}
     f16 = results.get("f16")
     if f16:
         line["contract_f16"] = {

@@ -8,7 +8,7 @@ Functions (C implementations in oracle.c, each citing the reference code it rest
   gemm_seq        CpuBackend::gemm accumulation, literal single-thread form
                   (crates/cpu/src/lib.rs:203-295, 606-691)
   gemm_fast       the same arithmetic, loop-interchanged and multi-threaded; bit-identical
-  gather_words    tests/permutation_test.rs:84-116
+  gather_words    tests/permutation_test.rs:84-116 (gather_words_mt: same words, threaded)
   contract_f64    tests/contraction_test.rs:200-268 (f64 accumulation, error magnitude)
   gate            tests/contraction_test.rs:280-313 accuracy gate
   north_star_tol  max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|
@@ -56,6 +56,9 @@ def lib():
                                           ctypes.POINTER(u64), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(ctypes.c_uint32)]
         L.oracle_gather_words.restype = u64
+        L.oracle_gather_words_mt.argtypes = L.oracle_gather_words.argtypes + [
+            ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+        L.oracle_gather_words_mt.restype = u64
         dp = ctypes.POINTER(ctypes.c_double)
         i64p = ctypes.POINTER(i64)
         u64p = ctypes.POINTER(u64)
@@ -123,6 +126,26 @@ def gather_words(words: np.ndarray, w: int, offset: int, shape, strides, conj=Fa
     got = lib().oracle_gather_words(words.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), w,
                                     offset, len(shape), sh, st, int(conj), int(complex_elem),
                                     out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    return out[:got]
+
+
+def gather_words_mt(words: np.ndarray, w: int, offset: int, shape, strides, conj=False,
+                    complex_elem=False, threads=None) -> np.ndarray:
+    """gather_words with the logical elements split into `threads` contiguous ranges."""
+    if threads is None:
+        threads = os.cpu_count() or 1
+    words = np.ascontiguousarray(words, dtype=np.uint32)
+    n = int(np.prod(shape, dtype=np.uint64)) if len(shape) else 1
+    out = np.zeros(max(n * w, 1), dtype=np.uint32)
+    sh = (ctypes.c_uint64 * max(len(shape), 1))(*shape)
+    st = (ctypes.c_uint64 * max(len(strides), 1))(*strides)
+    failed = ctypes.c_int(0)
+    got = lib().oracle_gather_words_mt(words.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), w,
+                                       offset, len(shape), sh, st, int(conj), int(complex_elem),
+                                       out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                       int(threads), ctypes.byref(failed))
+    if failed.value:
+        raise RuntimeError("oracle_gather_words_mt could not start its threads")
     return out[:got]
 
 

@@ -159,18 +159,22 @@ int oracle_gemm_fast_f32(uint64_t m, uint64_t n, uint64_t k, float alpha, float 
  * gather_words (tests/permutation_test.rs:84-116): the raw 32-bit words of a view in
  * row-major logical order; with `conj` on a complex (two-word) element the second word's
  * sign bit is flipped. `base` is the allocation as words; offset/strides in elements of
- * `w` words. Returns the number of words written.
+ * `w` words. gather_range writes logical elements [first, last) to out[first*w ...): an
+ * odometer over the view's indices started at `first`'s mixed-radix decomposition.
  */
-uint64_t oracle_gather_words(const uint32_t* base, uint32_t w, uint64_t offset, uint32_t rank,
-                             const uint64_t* shape, const uint64_t* strides, int conj,
-                             int complex_elem, uint32_t* out) {
-    uint64_t len = 1;
-    for (uint32_t d = 0; d < rank; ++d) len *= shape[d];
-    if (len == 0) return 0;
+static void gather_range(const uint32_t* base, uint32_t w, uint64_t offset, uint32_t rank,
+                         const uint64_t* shape, const uint64_t* strides, int conj,
+                         int complex_elem, uint64_t first, uint64_t last, uint32_t* out) {
+    if (first >= last) return;
     uint64_t idx[64];
     memset(idx, 0, sizeof(idx));
-    uint64_t written = 0;
-    for (;;) {
+    uint64_t rem = first;
+    for (uint32_t d = rank; d-- > 0;) {
+        idx[d] = rem % shape[d];
+        rem /= shape[d];
+    }
+    uint64_t written = first * w;
+    for (uint64_t i = first; i < last; ++i) {
         uint64_t e = offset;
         for (uint32_t d = 0; d < rank; ++d) e += idx[d] * strides[d];
         for (uint32_t kw = 0; kw < w; ++kw) {
@@ -178,14 +182,82 @@ uint64_t oracle_gather_words(const uint32_t* base, uint32_t w, uint64_t offset, 
             if (conj && complex_elem && kw == 1) word ^= 0x80000000u;
             out[written++] = word;
         }
-        uint32_t d = rank;
-        for (;;) {
-            if (d == 0) return written;
-            --d;
+        for (uint32_t d = rank; d-- > 0;) {
             if (++idx[d] < shape[d]) break;
             idx[d] = 0;
         }
     }
+}
+
+static uint64_t view_len(uint32_t rank, const uint64_t* shape) {
+    uint64_t len = 1;
+    for (uint32_t d = 0; d < rank; ++d) len *= shape[d];
+    return len;
+}
+
+/* Returns the number of words written (len * w). */
+uint64_t oracle_gather_words(const uint32_t* base, uint32_t w, uint64_t offset, uint32_t rank,
+                             const uint64_t* shape, const uint64_t* strides, int conj,
+                             int complex_elem, uint32_t* out) {
+    const uint64_t len = view_len(rank, shape);
+    gather_range(base, w, offset, rank, shape, strides, conj, complex_elem, 0, len, out);
+    return len * w;
+}
+
+typedef struct {
+    const uint32_t* base;
+    uint32_t w, rank;
+    uint64_t offset;
+    const uint64_t *shape, *strides;
+    int conj, complex_elem;
+    uint64_t first, last;
+    uint32_t* out;
+} gather_job;
+
+static void* gather_worker(void* arg) {
+    const gather_job* j = (const gather_job*)arg;
+    gather_range(j->base, j->w, j->offset, j->rank, j->shape, j->strides, j->conj,
+                 j->complex_elem, j->first, j->last, j->out);
+    return NULL;
+}
+
+/* The same words, with the logical elements split into `threads` contiguous ranges (every
+ * word lands where the one-thread form puts it). Returns the words written, or 0 with
+ * *failed set when a thread could not be started. */
+uint64_t oracle_gather_words_mt(const uint32_t* base, uint32_t w, uint64_t offset,
+                                uint32_t rank, const uint64_t* shape, const uint64_t* strides,
+                                int conj, int complex_elem, uint32_t* out, int threads,
+                                int* failed) {
+    const uint64_t len = view_len(rank, shape);
+    *failed = 0;
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    if ((uint64_t)threads > len) threads = len ? (int)len : 1;
+    gather_job jobs[256];
+    pthread_t tids[256];
+    for (int t = 0; t < threads; ++t) {
+        gather_job* j = &jobs[t];
+        j->base = base;
+        j->w = w;
+        j->rank = rank;
+        j->offset = offset;
+        j->shape = shape;
+        j->strides = strides;
+        j->conj = conj;
+        j->complex_elem = complex_elem;
+        j->first = len * (uint64_t)t / (uint64_t)threads;
+        j->last = len * (uint64_t)(t + 1) / (uint64_t)threads;
+        j->out = out;
+    }
+    int started[256] = {0};
+    for (int t = 1; t < threads; ++t)
+        started[t] = pthread_create(&tids[t], NULL, gather_worker, &jobs[t]) == 0;
+    gather_worker(&jobs[0]);
+    for (int t = 1; t < threads; ++t) {
+        if (started[t]) pthread_join(tids[t], NULL);
+        else *failed = 1;
+    }
+    return *failed ? 0 : len * w;
 }
 
 /*

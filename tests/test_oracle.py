@@ -307,6 +307,23 @@ def test_gather_offsets_strides_and_complex_words():
     assert oracle.gather_words(words, 1, 0, [3, 0], [1, 1]).size == 0
 
 
+def test_threaded_gather_writes_the_same_words():
+    """gather_words_mt (the all-core CPU baseline) against numpy and the one-thread form,
+    with range splits falling mid-row, more threads than elements, rank 0 and empty views."""
+    g = rng(5)
+    words = g.integers(0, 2 ** 32, 2 * 7 * 11 * 13, dtype=np.uint64).astype(np.uint32)
+    x = words[: 7 * 11 * 13].reshape(7, 11, 13)
+    for threads in (1, 2, 3, 7, 16, 2000):
+        got = oracle.gather_words_mt(words, 1, 0, [13, 7, 11], [1, 143, 13], threads=threads)
+        assert np.array_equal(got, np.transpose(x, (2, 0, 1)).ravel()), threads
+        cj = oracle.gather_words_mt(words, 2, 3, [5, 9], [1, 5], conj=True, complex_elem=True,
+                                    threads=threads)
+        assert np.array_equal(cj, oracle.gather_words(words, 2, 3, [5, 9], [1, 5], conj=True,
+                                                      complex_elem=True)), threads
+    assert oracle.gather_words_mt(words, 1, 9, [], [], threads=4).tolist() == [int(words[9])]
+    assert oracle.gather_words_mt(words, 1, 0, [3, 0], [1, 1], threads=4).size == 0
+
+
 def test_gather_reproduces_the_complex_adjoint_word_table():
     t = PKATS["complex_adjoint"]
     m, n = t["m"], t["n"]
