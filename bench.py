@@ -327,6 +327,18 @@ CPU_GEMM_SAMPLES = {"gemm4096": (48, None, 1), "c1": (512, None, 1), "c3": (32, 
                     "c4": (4, None, 1), "c5": (4, 256, 1)}
 
 
+def repeat_for(fn, min_s=0.25):
+    """Runs fn until at least min_s seconds have passed (at least once): (runs, seconds), so
+    the short samples are not timer noise."""
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        runs += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return runs, dt
+
+
 def cpu_gemm_rates(host, geom, seq_rows, fast_rows, fast_batches, threads):
     """crates/cpu's gemm restated (oracle/): the literal single-thread k-order loop on the
     first `seq_rows` output rows, and the bit-identical loop-interchanged variant on `threads`
@@ -339,17 +351,22 @@ def cpu_gemm_rates(host, geom, seq_rows, fast_rows, fast_batches, threads):
     a_st = (1, m) if a_t else (k, 1)
     b_st = (1, k) if b_t else (n, 1)
     c = np.zeros(m * n, np.float32)
-    t0 = time.perf_counter()
-    for r in range(seq_rows):
-        oracle.gemm_seq(1, n, k, 1.0, beta, a, r * a_st[0], a_st, b, 0, b_st, c, r * n, (n, 1))
-    seq = (2.0 * seq_rows * n * k, time.perf_counter() - t0)
+
+    def literal():
+        for r in range(seq_rows):
+            oracle.gemm_seq(1, n, k, 1.0, beta, a, r * a_st[0], a_st, b, 0, b_st, c, r * n,
+                            (n, 1))
     rows = None if fast_rows is None else np.arange(fast_rows, dtype=np.uint64)
     nr = (m if fast_rows is None else fast_rows) * fast_batches
-    t0 = time.perf_counter()
-    for bi in range(fast_batches):
-        oracle.gemm_fast(m, n, k, 1.0, beta, a, bi * m * k, a_st, b, bi * k * n, b_st, c, 0,
-                         (n, 1), rows=rows, threads=threads)
-    fast = (2.0 * nr * n * k, time.perf_counter() - t0)
+
+    def threaded():
+        for bi in range(fast_batches):
+            oracle.gemm_fast(m, n, k, 1.0, beta, a, bi * m * k, a_st, b, bi * k * n, b_st, c, 0,
+                             (n, 1), rows=rows, threads=threads)
+    runs, dt = repeat_for(literal)
+    seq = (2.0 * seq_rows * n * k * runs, dt, runs)
+    runs, dt = repeat_for(threaded)
+    fast = (2.0 * nr * n * k * runs, dt, runs)
     return seq, fast, (seq_rows, nr, batch * m)
 
 
@@ -362,12 +379,11 @@ def cpu_perm_rates(x, geom, threads):
     st = [int(np.prod(shape[d + 1:], dtype=np.int64)) for d in range(len(shape))]
     pshape, pst = [shape[p] for p in perm], [st[p] for p in perm]
     nbytes = 2.0 * words.size * 4
-    t0 = time.perf_counter()
-    oracle.gather_words(words, 1, 0, pshape, pst)
-    one = (nbytes, time.perf_counter() - t0)
-    t0 = time.perf_counter()
-    oracle.gather_words_mt(words, 1, 0, pshape, pst, threads=threads)
-    par = (nbytes, time.perf_counter() - t0)
+    runs, dt = repeat_for(lambda: oracle.gather_words(words, 1, 0, pshape, pst))
+    one = (nbytes * runs, dt, runs)
+    runs, dt = repeat_for(lambda: oracle.gather_words_mt(words, 1, 0, pshape, pst,
+                                                         threads=threads))
+    par = (nbytes * runs, dt, runs)
     return one, par
 
 
@@ -375,15 +391,18 @@ def attach_cpu_baselines(results, threads):
     """Adds cpu_baseline (one core, the literal restatement) and cpu_baseline_parallel
     (`threads` cores, bit-identical) to every GEMM and permutation workload, timed on bounded
     samples of the workload's own inputs after all GPU timing is done."""
+    def note(what, dt, runs):
+        return f"{what} ({runs} runs, {dt:.2f} s)" if runs > 1 else f"{what} ({dt:.2f} s)"
+
     def tf(work, what, cores):
-        flop, dt = work
+        flop, dt, runs = work
         return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-                "sample": f"{what} ({dt:.2f} s)"}
+                "sample": note(what, dt, runs)}
 
     def gb(work, what, cores):
-        nbytes, dt = work
+        nbytes, dt, runs = work
         return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-                "sample": f"{what} ({dt:.2f} s)"}
+                "sample": note(what, dt, runs)}
 
     for name, r in results.items():
         if not isinstance(r, dict):
@@ -393,7 +412,7 @@ def attach_cpu_baselines(results, threads):
             spec = CPU_GEMM_SAMPLES.get(name)
             if spec is None:
                 continue
-            tot = [[0.0, 0.0], [0.0, 0.0]]
+            tot = [[0.0, 0.0, 1], [0.0, 0.0, 1]]
             for p in parts:
                 seq, fast, (sr, fr, total_rows) = cpu_gemm_rates(p.pop("_host"), p.pop("_geom"),
                                                                  *spec, threads)
