@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstring>
+#include <memory>
 #include <sstream>
 
 #include "lg_internal.h"
@@ -185,13 +186,11 @@ lg_status lg_ctx_create(int32_t device, lg_ctx** out) {
             fail_no_device("device " + std::to_string(device) + " not present");
         }
         check_hip(hipSetDevice(device), "hipSetDevice");
-        hipStream_t s = nullptr;
-        check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
-        auto* ctx = new lg_ctx();
+        std::unique_ptr<lg_ctx> ctx(new lg_ctx());
         ctx->device = device;
-        ctx->stream = s;
         for (auto& n : ctx->names) n.store(nullptr);
-        *out = ctx;
+        check_hip(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
+        *out = ctx.release();
     });
 }
 

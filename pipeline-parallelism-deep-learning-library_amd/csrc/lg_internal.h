@@ -100,6 +100,13 @@ lg_status guarded(F&& body) {
     } catch (const std::bad_alloc&) {
         set_last_error("host allocation failed");
         return LG_KERNEL;
+    } catch (const std::exception& e) {
+        // Nothing may unwind through the C ABI; a library exception is an internal failure.
+        set_last_error(std::string("internal error: ") + e.what());
+        return LG_KERNEL;
+    } catch (...) {
+        set_last_error("internal error: unknown exception");
+        return LG_KERNEL;
     }
 }
 
