@@ -156,7 +156,9 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 1, 1>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);
     } else {
-        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 2, 2>), dim3(groups),
+        // A read along M (a transposed A) takes the two-ahead pipeline.
+        constexpr bool ahead = AM == LOAD_MN && BMD != LOAD_S;
+        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 2, 2, ahead>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);
     }
 }

@@ -492,6 +492,33 @@ def test_both_output_tiles_on_ragged_edges(ctx, pool):
         seed += 1
 
 
+def test_transposed_a_two_ahead_pipeline(ctx, pool):
+    """A read along M (transpose_matrix(X), the weight-gradient operand) takes the 128x128
+    kernel's two-slices-ahead pipeline: K with no complete follower slice, a branch-free
+    interior run followed by the general tail (partial last slice), exact slices, ragged
+    M/N edge tiles, split-K chunks, and both B layouts, against both oracles."""
+    seed = 6200
+    cases = [((2100, 2050, 37), (False,)), ((2080, 2050, 147), (False, True)),
+             ((2048, 2048, 96), (False,)), ((400, 300, 8192), (False, True))]
+    for (m, n, k), b_layouts in cases:
+        for tb in b_layouts:
+            alpha, beta = [(1.0, 0.0), (-0.75, 1.0), (0.5, -0.5)][seed % 3]
+            case = Case(f"A^T tb={tb} {m}x{n}x{k}", (Layout.transposed(m, k), "mk"),
+                        (Layout.transposed(k, n) if tb else Layout.dense([k, n]), "kn"),
+                        (Layout.dense([m, n]), "mn"), via_gemm=True)
+            plan = C.plan_gemm(alpha, _dummy_view(pool, case.a[0]), _dummy_view(pool, case.b[0]),
+                               beta, _dummy_view(pool, case.c[0]))
+            assert plan["tile"] == (128, 128) and plan["a_mode"] == "mn", plan
+            case.scalars(alpha, beta).run(ctx, pool, seed)
+            pool.free_all()
+            seed += 1
+
+
+def _dummy_view(pool, layout):
+    buf = pool.alloc("f32", layout.span() + 64)
+    return L.TensorView(buf, layout.offset, layout.shape, layout.strides, "f32")
+
+
 # --------------------------------------------------------------------------------------
 # BASELINE configurations at full size
 # --------------------------------------------------------------------------------------
