@@ -548,7 +548,7 @@ def main() -> int:
                             "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                             "frac": round(head["frac"], 4),
                             "traffic": traffic_from_profile("gemm4096"),
-                            "kernel": "gemm_f32_mfma<0, 1, 16, 2, 2> (A K-contiguous, B N-contiguous, 128x128 tile)",
+                            "kernel": "gemm_f32_mfma<0, 1, 16, 2, 2, false> (A K-contiguous, B N-contiguous, 128x128 tile)",
                             "profile": "profiles/gemm_f32_mfma_gemm4096.md, profiles/traffic_gemm4096.txt",
                             "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
     if head and "cpu_baseline" in head:
