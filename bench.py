@@ -327,6 +327,20 @@ CPU_GEMM_SAMPLES = {"gemm4096": (48, None, 1), "c1": (512, None, 1), "c3": (32, 
                     "c4": (4, None, 1), "c5": (4, 256, 1)}
 
 
+def host_cpu():
+    """The host the CPU baselines ran on: model name, logical CPUs, the threads used."""
+    model = "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(),
+            "threads_used": min(os.cpu_count() or 1, 16)}
+
+
 def repeat_for(fn, min_s=0.25):
     """Runs fn until at least min_s seconds have passed (at least once): (runs, seconds), so
     the short samples are not timer noise."""
@@ -586,6 +600,8 @@ def main() -> int:
             "peak_gbs": PEAK_GBS,
             "ops": {k_: {kk: (round(v, 4) if isinstance(v, float) else v) for kk, v in r.items()}
                     for k_, r in train.items()}}
+    if not args.no_cpu:
+        line["cpu_host"] = host_cpu()
     line["configs"] = {k_: {kk: (round(v, 4) if isinstance(v, float) else v)
                             for kk, v in r.items()} for k_, r in results.items()}
     print(json.dumps(line), flush=True)
