@@ -4,6 +4,13 @@ Every source is compiled with hipcc for gfx950 only. Device code is built with
 `-ffp-contract=off` (alpha*acc and beta*C round separately, as the reference's scalar rules
 are written) and with packed-FP32 instruction selection disabled. Run as a script or call
 `build()`; it always recompiles.
+
+`python build.py --host-sanitize DIR` builds a second library into DIR whose host code
+(planner, validation, wire parser, backend checks) carries AddressSanitizer and
+UndefinedBehaviorSanitizer, device code unchanged; the CPU test suite runs against it with
+  LD_PRELOAD=<clang asan runtime> PYTHONMALLOC=malloc ASAN_OPTIONS=detect_leaks=0 \
+  LINALG_HIP_LIB=DIR/liblinalg_hip.so python -m pytest tests -m "not gpu"
+(the runtime: /opt/rocm/llvm/lib/clang/<version>/lib/linux/libclang_rt.asan-x86_64.so).
 """
 from __future__ import annotations
 
@@ -39,12 +46,18 @@ DEVICE = [f"--offload-arch={ARCH}", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-def _compile(src: str) -> Path:
+SANITIZE = ["-Xarch_host", "-fsanitize=address,undefined", "-Xarch_host",
+            "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer", "-g"]
+
+
+def _compile(src: str, obj: Path = OBJ, sanitize: bool = False) -> Path:
     path = CSRC / src
-    out = OBJ / (src + ".o")
+    out = obj / (src + ".o")
     cmd = [HIPCC, *COMMON]
     if src.endswith(".hip"):
         cmd += DEVICE
+    elif sanitize:
+        cmd += SANITIZE
     cmd += ["-c", str(path), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -68,6 +81,25 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_host_sanitized(out_dir: Path) -> Path:
+    out_dir = Path(out_dir)
+    obj = out_dir / "_build"
+    obj.mkdir(parents=True, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
+        objs = list(pool.map(lambda s: _compile(s, obj, True), SOURCES))
+    lib = out_dir / "liblinalg_hip.so"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libasan",
+           "-Xarch_host", "-fsanitize=address,undefined", "-o", str(lib), *[str(o) for o in objs]]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    print(f"built {lib}")
+    return lib
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if len(sys.argv) == 3 and sys.argv[1] == "--host-sanitize":
+        build_host_sanitized(Path(sys.argv[2]))
+    else:
+        build(verbose=True)
     sys.exit(0)

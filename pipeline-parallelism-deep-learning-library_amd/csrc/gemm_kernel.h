@@ -447,7 +447,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_small(GemmArgs p) {
     __syncthreads();
     float* C = p.c + static_cast<int64_t>(plane) * p.c_sb;
 #pragma unroll
-    for (int j = 0; j < SMALL_TILE * SMALL_TILE / GEMM_THREADS; ++j) {
+    for (int j = 0; j < SMALL_TILE * SMALL_TILE / static_cast<int>(GEMM_THREADS); ++j) {
         const int e = j * GEMM_THREADS + tid;
         const uint32_t row = m0 + e / SMALL_TILE, col = n0 + e % SMALL_TILE;
         if (inner || (row < p.m && col < p.n)) {
