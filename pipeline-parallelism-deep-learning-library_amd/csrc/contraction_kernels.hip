@@ -13,6 +13,7 @@ namespace {
 
 using gemm_detail::gemm_f32_mfma;
 using gemm_detail::gemm_f32_small;
+using gemm_detail::SMALL_WAVES;
 
 // Split-K second pass. Partials are [batch][splits][m][n], dense. A workgroup owns 64 runs
 // of V consecutive outputs; its four waves each sum a fixed quarter of the splits in
@@ -151,7 +152,8 @@ void check_launch(const char* what) { check_hip(hipGetLastError(), what); }
 template <int AM, int BMD>
 void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
     if (a.tile == GEMM_TINY_TILE) {
-        hipLaunchKernelGGL((gemm_f32_small<AM, BMD>), dim3(groups), dim3(GEMM_THREADS), 0, s, a);
+        hipLaunchKernelGGL((gemm_f32_small<AM, BMD, SMALL_WAVES>), dim3(groups), dim3(64 * SMALL_WAVES), 0,
+                           s, a);
     } else if (a.tile == GEMM_SMALL_TILE) {
         hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 1, 1>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);

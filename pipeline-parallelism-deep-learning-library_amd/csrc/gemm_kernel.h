@@ -371,14 +371,17 @@ void gemm_f32_mfma(GemmArgs p) {
 }
 
 // Small products (the 64x64 grid alone under 256 tiles, K <= GEMM_SMALL_K): one 32x32 output
-// tile per 256-thread workgroup in a single launch. The four waves take interleaved 8-k
-// groups (wave w: groups w, w+4, ...), each accumulating one v_mfma_f32_32x32x2_f32 block
-// straight from registers: the 32 rows are shared by the waves but their k ranges are not,
-// so there is nothing for LDS to reuse. Lane (r = lane%32, h = lane/32) holds k = 8g + 4h + s
-// at MFMA step s, as in the tiled kernel; an operand contiguous along K gives it a 128-bit
-// load, one contiguous along M/N four 32-bit loads that coalesce across lanes. The four wave
-// sums meet in LDS and add in wave order, then beta*C + sum: the order depends on K alone.
+// tile per workgroup of W waves in a single launch. The waves take interleaved 8-k groups
+// (wave w: groups w, w+W, ...), each accumulating one v_mfma_f32_32x32x2_f32 block straight
+// from registers: the 32 rows are shared by the waves but their k ranges are not, so there is
+// nothing for LDS to reuse. Lane (r = lane%32, h = lane/32) holds k = 8g + 4h + s at MFMA
+// step s, as in the tiled kernel; an operand contiguous along K gives it a 128-bit load, one
+// contiguous along M/N four 32-bit loads that coalesce across lanes. The W wave sums meet in
+// LDS and add in wave order, then beta*C + sum: the order depends on K and W alone. The
+// launch uses W = 16 (four waves per SIMD): with K = 512 each wave issues all of its loads at
+// once and the SIMD interleaves four accumulation chains (config 1: 33 -> 38 TFLOP/s).
 constexpr int SMALL_TILE = 32;
+constexpr int SMALL_WAVES = 16;  // waves per small-product workgroup
 constexpr int SMALL_UNROLL = 4;  // 8-k groups whose loads are issued before their MFMAs
 
 template <int MODE, bool FULL>
@@ -397,9 +400,10 @@ __device__ inline floatx4 small_frag(const float* __restrict__ p, int64_t srow, 
     return v;
 }
 
-template <int AM, int BMD>
-__global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_small(GemmArgs p) {
-    __shared__ float red[4][SMALL_TILE * SMALL_TILE];
+template <int AM, int BMD, int W = 4>
+__global__ __launch_bounds__(64 * W) void gemm_f32_small(GemmArgs p) {
+    constexpr int THREADS = 64 * W;
+    __shared__ float red[W][SMALL_TILE * SMALL_TILE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 31, h = lane >> 5;
     uint32_t plane, tm, tn;
@@ -414,21 +418,21 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_small(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
     const uint32_t groups = (p.k + 7) / 8;
-    // Batches of SMALL_UNROLL of this wave's groups: g = wave + 4 * (b * SMALL_UNROLL + u).
-    for (uint32_t g0 = wave; g0 < groups; g0 += 4 * SMALL_UNROLL) {
+    // Batches of SMALL_UNROLL of this wave's groups: g = wave + W * (b * SMALL_UNROLL + u).
+    for (uint32_t g0 = wave; g0 < groups; g0 += W * SMALL_UNROLL) {
         floatx4 av[SMALL_UNROLL], bv[SMALL_UNROLL];
-        const uint32_t last = g0 + 4 * (SMALL_UNROLL - 1);
+        const uint32_t last = g0 + W * (SMALL_UNROLL - 1);
         if (inner && 8 * last + 8 <= p.k) {
 #pragma unroll
             for (int u = 0; u < SMALL_UNROLL; ++u) {
-                const uint32_t k0 = 8 * (g0 + 4 * u);
+                const uint32_t k0 = 8 * (g0 + W * u);
                 av[u] = small_frag<AM, true>(A, p.a_sm, p.a_sk, true, k0, p.k, r, h);
                 bv[u] = small_frag<BMD, true>(B, p.b_sn, p.b_sk, true, k0, p.k, r, h);
             }
         } else {
 #pragma unroll
             for (int u = 0; u < SMALL_UNROLL; ++u) {
-                const uint32_t k0 = 8 * (g0 + 4 * u);  // past K: every element predicated to 0
+                const uint32_t k0 = 8 * (g0 + W * u);  // past K: every element predicated to 0
                 av[u] = small_frag<AM, false>(A, p.a_sm, p.a_sk, a_ok, k0, p.k, r, h);
                 bv[u] = small_frag<BMD, false>(B, p.b_sn, p.b_sk, b_ok, k0, p.k, r, h);
             }
@@ -447,11 +451,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_f32_small(GemmArgs p) {
     __syncthreads();
     float* C = p.c + static_cast<int64_t>(plane) * p.c_sb;
 #pragma unroll
-    for (int j = 0; j < SMALL_TILE * SMALL_TILE / static_cast<int>(GEMM_THREADS); ++j) {
-        const int e = j * GEMM_THREADS + tid;
+    for (int j = 0; j < SMALL_TILE * SMALL_TILE / THREADS; ++j) {
+        const int e = j * THREADS + tid;
         const uint32_t row = m0 + e / SMALL_TILE, col = n0 + e % SMALL_TILE;
         if (inner || (row < p.m && col < p.n)) {
-            float v = ((red[0][e] + red[1][e]) + red[2][e]) + red[3][e];
+            float v = red[0][e];
+#pragma unroll
+            for (int w = 1; w < W; ++w) v = v + red[w][e];
             float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
             if (p.beta != 0.0f) v = p.beta * *q + v;
             *q = v;
