@@ -514,6 +514,26 @@ def test_transposed_a_two_ahead_pipeline(ctx, pool):
             seed += 1
 
 
+def test_transposed_a_pipeline_is_deterministic(ctx, pool):
+    """The two-ahead pipeline with split-K chunks (A read along M) gives the same bits on
+    three runs, with beta = 1 accumulating into the same starting C each time."""
+    m, n, k = 400, 300, 8192
+    g = rng(6300)
+    a = Tensor.random(pool, Layout.transposed(m, k), g)
+    b = Tensor.random(pool, Layout.dense([k, n]), g)
+    c = Tensor.random(pool, Layout.dense([m, n]), g)
+    c0 = c.host.copy()
+    plan = C.plan_gemm(0.5, a.view(), b.view(), 1.0, c.view())
+    assert plan["tile"] == (128, 128) and plan["a_mode"] == "mn" and plan["splits"] > 1, plan
+    outs = []
+    for _ in range(3):
+        c.host[:] = c0
+        c.upload()
+        C.gemm(ctx, 0.5, a.view(), b.view(), 1.0, c.view())
+        outs.append(c.read().view(np.uint32).copy())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
 def _dummy_view(pool, layout):
     buf = pool.alloc("f32", layout.span() + 64)
     return L.TensorView(buf, layout.offset, layout.shape, layout.strides, "f32")
