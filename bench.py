@@ -458,7 +458,8 @@ def main() -> int:
                          "of sustained MFMA load to reach its steady clock (5 launches of the "
                          "4096^3 GEMM measure ~7%% below steady state)")
     ap.add_argument("--only", default=None,
-                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, copy, t8191, train, f16")
+                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, "
+                         "train, f16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -523,6 +524,9 @@ def main() -> int:
                                   [64, 128, 64, 32], [0, 2, 3, 1], 3, args))
     run("c2b", lambda: bench_perm(ctx, events, pool, L, P, "C2b [512,1024,256] perm (2,0,1)",
                                   [512, 1024, 256], [2, 0, 1], 4, args))
+    # The other reading of the "1 GiB" permutation target: a 1 GiB tensor (2 GiB moved).
+    run("c2b_1g", lambda: bench_perm(ctx, events, pool, L, P, "[1024,1024,256] perm (2,0,1), 1 GiB tensor",
+                                     [1024, 1024, 256], [2, 0, 1], 5, args))
     run("copy", lambda: {"name": "plain 128-bit copy 512 MiB", "gbs": bench_copy(ctx, events, pool,
                                                                                  L, P, 1 << 27, args)})
     def t8191():

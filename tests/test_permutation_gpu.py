@@ -335,7 +335,8 @@ def test_rejects_invalid_metadata_without_launching(ctx, pool):
 # BASELINE configurations at full size: bit-exact against numpy.transpose of the raw words.
 # --------------------------------------------------------------------------------------
 @pytest.mark.parametrize("shape,perm,seed", [([64, 128, 64, 32], [0, 2, 3, 1], 3),
-                                             ([512, 1024, 256], [2, 0, 1], 4)])
+                                             ([512, 1024, 256], [2, 0, 1], 4),
+                                             ([1024, 1024, 256], [2, 0, 1], 5)])
 def test_baseline_configs_full_size_bit_exact(ctx, pool, shape, perm, seed):
     n = int(np.prod(shape))
     g = rng(seed)
