@@ -422,3 +422,34 @@ def test_f16_plans_and_validation():
     cv = L.TensorView(shared, 64, [64, 32], [32, 1], "f16")
     with pytest.raises(L.Overlap):
         C.plan_gemm(1.0, av, b, 0.0, cv)
+
+
+def test_missing_library_fails_loudly_and_there_is_no_cpu_fallback():
+    """With the HIP library absent the package raises ImportError at first use; nothing
+    computes on the CPU in its place."""
+    import os
+    import subprocess
+    import sys
+    code = ("import linalg_hip as L\n"
+            "try:\n"
+            "    L.Context.new(0)\n"
+            "except ImportError as e:\n"
+            "    print('ImportError', 'no CPU fallback' in str(e))\n")
+    env = dict(os.environ, LINALG_HIP_LIB="/nonexistent/liblinalg_hip.so")
+    pkg = str(GOLDEN.parent.parent / "pipeline-parallelism-deep-learning-library_amd")
+    env["PYTHONPATH"] = pkg + os.pathsep + env.get("PYTHONPATH", "")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.stdout.strip() == "ImportError True", (out.stdout, out.stderr[-2000:])
+
+
+def test_context_without_a_device_is_no_device():
+    """lg_ctx_create on a machine without a usable GPU returns LG_NO_DEVICE (MetalContext::new's
+    NoDevice, src/abi.rs:56-62) and sets the thread's last error."""
+    import os
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU driver is present")
+    ctx = ctypes.c_void_p()
+    st = N.lib().lg_ctx_create(0, ctypes.byref(ctx))
+    assert st == 1 and not ctx.value  # LG_NO_DEVICE
+    assert b"no HIP device" in N.lib().lg_last_error()
