@@ -186,6 +186,22 @@ __device__ inline double hval(const uint16_t* __restrict__ st, int row, int k) {
     return widen<HK>(MODE == LOAD_MN ? st[k * HP + row] : st[row * HP + k]);
 }
 
+// Elements (row, k0 .. k0+3) of a stage, widened exactly: one 64-bit LDS read from a
+// [row][k] stage (k0 is a multiple of four, rows are 144 bytes), four 16-bit reads from a
+// [k][row] one.
+template <int MODE, int HK>
+__device__ inline void hval4(double (&v)[4], const uint16_t* __restrict__ st, int row, int k0) {
+    if constexpr (MODE == LOAD_MN) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = widen<HK>(st[(k0 + j) * HP + row]);
+    } else {
+        typedef uint16_t h4 __attribute__((ext_vector_type(4)));
+        const h4 w = *reinterpret_cast<const h4*>(st + row * HP + k0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = widen<HK>(w[j]);
+    }
+}
+
 template <int AM, int BMD, int HK>
 __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[4 * H_STAGE];
@@ -230,18 +246,24 @@ __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
         if (more) load((kt + 1) * HGEMM_BK);
         const uint16_t* as = As + s * H_STAGE;
         const uint16_t* bs = Bs + s * H_STAGE;
-#pragma unroll 4
-        for (int ks = 0; ks < HGEMM_BK / 4; ++ks) {
-            double av[2], bv[2];
+        // 16-k groups: MFMA step s of group q gives lane group lk the k = 16q + 4lk + s, so
+        // a [row][k] stage hands a lane its four k of the group in one 64-bit read. A and B
+        // agree on the order, so every product pairs the same k.
+#pragma unroll 1
+        for (int q = 0; q < HGEMM_BK / 16; ++q) {
+            double av[2][4], bv[2][4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) av[i] = hval<AM, HK>(as, wm * 32 + i * 16 + li, ks * 4 + lk);
+            for (int i = 0; i < 2; ++i) hval4<AM, HK>(av[i], as, wm * 32 + i * 16 + li, q * 16 + lk * 4);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bv[j] = hval<BMD, HK>(bs, wn * 32 + j * 16 + li, ks * 4 + lk);
+            for (int j = 0; j < 2; ++j) hval4<BMD, HK>(bv[j], bs, wn * 32 + j * 16 + li, q * 16 + lk * 4);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int st = 0; st < 4; ++st)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bv[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i][st], bv[j][st],
+                                                                         acc[i][j], 0, 0, 0);
         }
         if (more) {
             hstage(As + (s ^ 1) * H_STAGE, ra, tid);
