@@ -5,7 +5,7 @@ Prints ONE JSON line. The headline (`value`) is fp32 contraction TFLOP/s on the 
 workload, C[4096,4096] = A[4096,4096] . B[4096,4096] row-major (a "step" is one such
 contraction over resident HBM inputs). The same line carries the permutation headline
 (GB/s on the 1 GiB-traffic [512,1024,256] perm (2,0,1) materialization) and every
-BASELINE configuration, each with its roofline fraction:
+benchmark configuration, each with its roofline fraction:
   contraction: achieved = 2*B*M*N*K / mean kernel time, peak = 157.3 TFLOP/s fp32 MFMA
   permutation: achieved = 2*numel*4 B / mean kernel time,  peak = 8000 GB/s HBM
 Kernel time is measured with HIP events recorded on the stream the kernels are launched on,

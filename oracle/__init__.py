@@ -225,7 +225,7 @@ def gate(got_buffer: np.ndarray, expected: Expected, name: str = "") -> dict:
 
 
 def north_star_tol(k: int, a: np.ndarray, b: np.ndarray) -> float:
-    """max|err| <= 1e-5 * sqrt(K) * max|a| * max|b| (fp32)."""
+    """max|err| <= 1e-5 * sqrt(K) * max|a| * max|b| (the fp32 north-star bound)."""
     ma = float(np.max(np.abs(a))) if a.size else 0.0
     mb = float(np.max(np.abs(b))) if b.size else 0.0
     return 1e-5 * max(k, 1) ** 0.5 * ma * mb

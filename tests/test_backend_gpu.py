@@ -235,7 +235,7 @@ def test_repeated_gemm_is_bitwise_stable_and_transposes_are_read_in_place(hb):
 
 def test_pipeline_stage_linear_step(hb):
     """One 1F1B stage's linear layer through the backend: Y = X.W, dX = dY.W^T, dW = X^T.dY
-    (the fifth BASELINE configuration at reduced size; the operands are transpose_matrix
+    (the fifth benchmark configuration at reduced size; the operands are transpose_matrix
     views of the stored row-major tensors, read in place)."""
     mb, d, h = 256, 384, 640
     g = rng(5)

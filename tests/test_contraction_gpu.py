@@ -7,7 +7,7 @@ and, for 2-D gemm cases, against the crates/cpu restatement with the north-star 
   max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|.
 Every buffer element outside C's view must keep its bits; with beta = 0, C starts as NaN.
 The case list restates tests/contraction_test.rs (the 20 typed cases for f32 and the 96-case
-random sweep); the BASELINE configurations run at full size with row samples checked against
+random sweep); the benchmark configurations run at full size with row samples checked against
 the oracle and size-independent properties (determinism, linearity) on the whole output.
 """
 from __future__ import annotations
@@ -540,7 +540,7 @@ def _dummy_view(pool, layout):
 
 
 # --------------------------------------------------------------------------------------
-# BASELINE configurations at full size
+# benchmark configurations at full size
 # --------------------------------------------------------------------------------------
 def _rows_check(name, got_rows, want_rows, k, amax, bmax):
     tol = 1e-5 * np.sqrt(k) * amax * bmax

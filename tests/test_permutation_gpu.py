@@ -3,7 +3,7 @@
 Restates the cases of tests/permutation_test.rs over the C ABI: destinations start as
 SENTINEL words and every word outside the destination view must survive; sources mix random
 words and SPECIALS (NaN payloads, -0, infinities, subnormals); all element types (f32, u32,
-complex f32). The BASELINE configurations run at full size and are compared word for word
+complex f32). The benchmark configurations run at full size and are compared word for word
 with numpy.transpose of the raw bits.
 """
 from __future__ import annotations
@@ -332,7 +332,7 @@ def test_rejects_invalid_metadata_without_launching(ctx, pool):
 
 
 # --------------------------------------------------------------------------------------
-# BASELINE configurations at full size: bit-exact against numpy.transpose of the raw words.
+# benchmark configurations at full size: bit-exact against numpy.transpose of the raw words.
 # --------------------------------------------------------------------------------------
 @pytest.mark.parametrize("shape,perm,seed", [([64, 128, 64, 32], [0, 2, 3, 1], 3),
                                              ([512, 1024, 256], [2, 0, 1], 4),
