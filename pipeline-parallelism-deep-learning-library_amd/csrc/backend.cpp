@@ -193,6 +193,9 @@ lg_core_error run_op(F&& body) {
     } catch (const std::exception& e) {
         set_last_error(e.what());
         return LG_CORE_UNSUPPORTED_DEVICE;
+    } catch (...) {
+        set_last_error("internal error: unknown exception");
+        return LG_CORE_UNSUPPORTED_DEVICE;
     }
 }
 
@@ -415,6 +418,12 @@ extern "C" lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_ten
         return e.code;
     } catch (const Failure& f) {
         set_last_error(f.message);
+        return LG_CORE_UNSUPPORTED_DEVICE;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return LG_CORE_UNSUPPORTED_DEVICE;
+    } catch (...) {
+        set_last_error("internal error: unknown exception");
         return LG_CORE_UNSUPPORTED_DEVICE;
     }
 }

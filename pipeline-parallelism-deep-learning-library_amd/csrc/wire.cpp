@@ -123,6 +123,12 @@ lg_core_error wire_op(F&& body) {
     } catch (const Failure& f) {
         set_last_error(f.message);
         return LG_CORE_UNSUPPORTED_DEVICE;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return LG_CORE_UNSUPPORTED_DEVICE;
+    } catch (...) {
+        set_last_error("internal error: unknown exception");
+        return LG_CORE_UNSUPPORTED_DEVICE;
     }
 }
 
