@@ -391,7 +391,7 @@ typedef struct lg_contract_plan {
     uint64_t scratch_bytes; /* device scratch of the split-K partials */
     uint32_t tile_m;      /* output tile of one workgroup (tiled/split): 128x128; 64x64 when */
     uint32_t tile_n;      /* 128x128 tiles would leave most compute units idle; 32x32 (one
-                             launch, the four waves splitting K) for small outputs with
+                             launch, sixteen waves splitting K) for small outputs with
                              K <= 1024; f16: 64x64 */
 } lg_contract_plan;
 
