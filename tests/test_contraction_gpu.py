@@ -514,6 +514,20 @@ def test_transposed_a_two_ahead_pipeline(ctx, pool):
             seed += 1
 
 
+def test_transposed_a_pipeline_batched(ctx, pool):
+    """Batched products whose A is read along M take the same two-ahead kernel per batch
+    plane: four 1024x1024x256 planes (256 tiles of 128x128, no split-K)."""
+    b, m, n, k = 4, 1024, 1024, 256
+    case = Case("batched A^T", (Layout.with_([b, m, k], [0, 2, 1], [1, 1, 1], 0), "bmk"),
+                (Layout.dense([b, k, n]), "bkn"), (Layout.dense([b, m, n]), "bmn"))
+    plan = C.plan_contract(0.5, (_dummy_view(pool, case.a[0]), "bmk"),
+                           (_dummy_view(pool, case.b[0]), "bkn"), 1.0,
+                           (_dummy_view(pool, case.c[0]), "bmn"))
+    assert plan["tile"] == (128, 128) and plan["a_mode"] == "mn" and plan["splits"] == 1, plan
+    pool.free_all()
+    case.scalars(0.5, 1.0).run(ctx, pool, 6400)
+
+
 def test_transposed_a_pipeline_is_deterministic(ctx, pool):
     """The two-ahead pipeline with split-K chunks (A read along M) gives the same bits on
     three runs, with beta = 1 accumulating into the same starting C each time."""
