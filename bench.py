@@ -197,6 +197,116 @@ def bench_copy(ctx, events, pool, L, P, n, args):
     return 2.0 * n * 4 / (ms * 1e-3) / 1e9
 
 
+def bench_contract(ctx, events, pool, L, C, name, a_spec, b_spec, c_spec, args, seed=42):
+    """One contraction of the reference's own benchmark list (tests/contraction_test.rs:
+    1293-1395, bench_other_paths): each spec is (shape, strides, labels), inputs uniform in
+    [-1, 1), beta = 0. FLOP = 2 * product of every label's extent; algorithmic bytes = A and B
+    read once plus C written once. The roofline is whichever of the fp32 MFMA peak and the HBM
+    peak binds at that intensity."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    bufs, views, host = [], [], []
+    for i, (shape, strides, labels) in enumerate((a_spec, b_spec, c_spec)):
+        span = 1 + sum((e - 1) * st for e, st in zip(shape, strides))
+        buf = pool.alloc("f32", span)
+        if i < 2:
+            x = g.uniform(-1, 1, span).astype(np.float32)
+            buf.write(x)
+            host.append(x)
+        views.append((L.TensorView(buf, 0, shape, strides), labels))
+    extents = {}
+    for (v, labels) in views:
+        extents.update(zip(labels, v.shape))
+    flops = 2.0 * float(np.prod([float(e) for e in extents.values()]))
+    nbytes = 4.0 * sum(float(np.prod(v.shape)) for v, _ in views)
+    plan = C.plan_contract(1.0, views[0], views[1], 0.0, views[2])
+    C.encode_contract(ctx, ctx.queue, 1.0, views[0], views[1], 0.0, views[2])
+    (av, la), (bv, lb), (cv, lc) = views
+    launch = abi_call(native_lib().lg_encode_contract_f32, ctx.handle, ctx.queue.handle,
+                      ctypes.c_float(1.0), av.to_c(), la.encode(), bv.to_c(), lb.encode(),
+                      ctypes.c_float(0.0), cv.to_c(), lc.encode())
+    ms = timed(ctx, events, launch, args.steps, args.warmup)
+    med, best = per_launch(ctx, events, launch, args.steps)
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    mfma_bound = flops / (PEAK_TFLOPS * 1e12) >= nbytes / (PEAK_GBS * 1e9)
+    roof = ({"bound": "mfma", "achieved": tflops, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+             "frac": tflops / PEAK_TFLOPS} if mfma_bound else
+            {"bound": "hbm", "achieved": gbs, "peak": PEAK_GBS, "unit": "GB/s",
+             "frac": gbs / PEAK_GBS})
+    return {"name": name, "ms": ms, "ms_median": med, "ms_best": best, "host_ms": HOST_MS[launch],
+            "tflops": tflops, "gbs": gbs, "flop": flops, "bytes": nbytes, "roofline": roof,
+            "plan": {k_: plan[k_] for k_ in ("kind", "kernel", "tile", "a_mode", "b_mode",
+                                              "splits", "workgroups", "swapped")},
+            "_other": (host, [(v.shape, v.strides, l) for v, l in views])}
+
+
+def other_paths_specs():
+    """(key, name, a, b, c) of the reference's bench_other_paths (tests/contraction_test.rs:
+    1293-1395); shapes with their strides and labels."""
+    def dense(shape):
+        st, p = [], 1
+        for e in reversed(shape):
+            st.append(p)
+            p *= e
+        return list(shape), st[::-1]
+
+    def cm(r, c):  # Layout::transposed(rows, cols): column-major
+        return [r, c], [1, r]
+    n2, k16, k1 = 2048, 1 << 24, 1 << 20
+    return [
+        ("o_t2048", "transposed 2048 (A, B, C column-major)", (*cm(n2, n2), "mk"),
+         (*cm(n2, n2), "kn"), (*cm(n2, n2), "mn")),
+        ("o_batched", "batched 4096 x 32^3", (*dense([4096, 32, 32]), "bmk"),
+         (*dense([4096, 32, 32]), "bkn"), (*dense([4096, 32, 32]), "bmn")),
+        ("o_dot", "dot K=16M", (*dense([1, k16]), "mk"), (*dense([k16, 1]), "kn"),
+         (*dense([1, 1]), "mn")),
+        ("o_32k1m", "32x32 K=1M (B column-major)", (*dense([32, k1]), "mk"), (*cm(k1, 32), "kn"),
+         (*dense([32, 32]), "mn")),
+        ("o_rank1", "rank-1 4096^2", (*dense([4096, 1]), "mk"), (*dense([1, 4096]), "kn"),
+         (*dense([4096, 4096]), "mn")),
+        ("o_rank4", "rank-4 ijkl,klmn->ijmn 48^6", (*dense([48] * 4), "ijkl"),
+         (*dense([48] * 4), "klmn"), (*dense([48] * 4), "ijmn")),
+    ]
+
+
+def cpu_other_rate(host, specs):
+    """The literal crates/cpu loop (oracle.gemm_seq, one core) on a bounded sample of one
+    bench_other_paths workload, on its own inputs: (FLOP, seconds, runs, what). Batched and
+    merged-axis workloads run as the 2-D products crates/cpu would be called with."""
+    import oracle
+    (a_shape, a_st, la), (b_shape, b_st, lb), (c_shape, c_st, lc) = specs
+    x, y = host
+    if la == "bmk":  # one 32x32x32 product per batch: a sample of 256 batches
+        bm, m, k = a_shape
+        n = b_shape[2]
+        c = np.zeros(m * n, np.float32)
+        nb = 256
+
+        def run():
+            for i in range(nb):
+                oracle.gemm_seq(m, n, k, 1.0, 0.0, x, i * m * k, (k, 1), y, i * k * n, (n, 1), c, 0,
+                                (n, 1))
+        what, flop = f"{nb} of {bm} batches", 2.0 * nb * m * n * k
+    else:
+        if la == "ijkl":
+            e = a_shape[0] * a_shape[1]
+            m = n = k = e
+            sa, sb, sc = (e, 1), (e, 1), (e, 1)
+        else:
+            m, k = a_shape
+            n = b_shape[1]
+            sa, sb, sc = tuple(a_st), tuple(b_st), tuple(c_st)
+        rows = max(1, min(m, int(2e8 // max(1, 2 * n * k))))  # about 0.2 GFLOP
+        c = np.zeros(max(m * n, 1), np.float32)
+
+        def run():
+            for r in range(rows):
+                oracle.gemm_seq(1, n, k, 1.0, 0.0, x, r * sa[0], sa, y, 0, sb, c, r * sc[0], sc)
+        what, flop = f"{rows} of {m} output rows", 2.0 * rows * n * k
+    runs, dt = repeat_for(run)
+    return flop * runs, dt, runs, what
+
+
 def bench_gemm_f16(ctx, events, pool, L, C, m, n, k, args):
     """f16 contraction (each output rounded once from an f64 dot on the f64 matrix cores):
     TFLOP/s against the 78.6 TFLOP/s f64 MFMA peak the kernel runs on."""
@@ -214,6 +324,8 @@ def bench_gemm_f16(ctx, events, pool, L, C, m, n, k, args):
                args.steps, args.warmup)
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     res = {"name": f"f16 gemm {m}x{n}x{k} (f64 accumulation, one f16 rounding)", "ms": ms,
+           "ms_median": per_launch(ctx, events, lambda: C.encode_gemm(ctx, ctx.queue, 1.0, av, bv,
+                                                                     0.0, cv), args.steps)[0],
            "tflops": tf, "frac_f64_mfma": tf / PEAK_F64_TFLOPS,
            "plan": {k_: plan[k_] for k_ in ("kind", "workgroups")}}
     if not args.no_cpu:
@@ -421,6 +533,10 @@ def attach_cpu_baselines(results, threads):
     for name, r in results.items():
         if not isinstance(r, dict):
             continue
+        if "_other" in r:
+            flop, dt, runs, what = cpu_other_rate(*r.pop("_other"))
+            r["cpu_baseline"] = tf((flop, dt, runs), f"{what}, literal k-order loop", 1)
+            continue
         parts = r.get("parts") or [r]
         if all("_geom" in p and isinstance(p["_host"], tuple) for p in parts):
             spec = CPU_GEMM_SAMPLES.get(name)
@@ -459,7 +575,8 @@ def main() -> int:
                          "4096^3 GEMM measure ~7%% below steady state)")
     ap.add_argument("--only", default=None,
                     help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, "
-                         "train, f16")
+                         "train, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, o_rank4, "
+                         "o_f16_2048")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -538,10 +655,16 @@ def main() -> int:
         r.pop("_geom")
         r["copy_gbs"] = bench_copy(ctx, events, pool, L, P, 8191 * 4099, args)
         r["ratio_vs_copy"] = r["gbs"] / r["copy_gbs"]
+        r["reference_gate"] = {"min_ratio_vs_copy": 0.70, "passed": r["ratio_vs_copy"] >= 0.70,
+                               "source": "tests/permutation_test.rs:741-792"}
         return r
     run("t8191", t8191)
     run("train", lambda: bench_train_ops(events, args, timed))
     run("f16", lambda: bench_gemm_f16(ctx, events, pool, L, C, 4096, 4096, 4096, args))
+    # The reference's own benchmark list (tests/contraction_test.rs:1293-1395).
+    for key, name, a_spec, b_spec, c_spec in other_paths_specs():
+        run(key, lambda: bench_contract(ctx, events, pool, L, C, name, a_spec, b_spec, c_spec, args))
+    run("o_f16_2048", lambda: bench_gemm_f16(ctx, events, pool, L, C, 2048, 2048, 2048, args))
 
     train = results.pop("train", None)
     if not args.no_cpu:
@@ -551,6 +674,7 @@ def main() -> int:
         for p in ([r] + list(r.get("parts", []))) if isinstance(r, dict) else []:
             p.pop("_host", None)
             p.pop("_geom", None)
+            p.pop("_other", None)
 
     head = results.get("gemm4096")
     perm = results.get("c2b")

@@ -369,8 +369,18 @@ typedef enum lg_plan_kind {
     LG_PLAN_SCALE = 2,   /* Fill with beta != 0: C = beta * C */
     LG_PLAN_TILED = 3,   /* one MFMA GEMM launch */
     LG_PLAN_SPLIT = 4,   /* split-K MFMA partials + ordered reduction */
-    LG_PLAN_GENERAL = 5  /* mixed-radix fallback (more than one stride per group) */
+    LG_PLAN_GENERAL = 5, /* mixed-radix fallback (more than one stride per group) */
+    LG_PLAN_DOT = 6      /* M = N = 1: VALU dot products, split along K with ordered partials */
 } lg_plan_kind;
+
+/* Kernel of a tiled, split or dot plan. */
+typedef enum lg_plan_kernel {
+    LG_KERNEL_NONE = 0,  /* empty, fill or general plans */
+    LG_KERNEL_TILE = 1,  /* 128x128 (or 64x64) output tile per 256-thread workgroup */
+    LG_KERNEL_SMALL = 2, /* one 32x32 tile per workgroup, sixteen waves splitting its K */
+    LG_KERNEL_WAVE = 3,  /* one 32x32 tile per wave (batches of small products) */
+    LG_KERNEL_DOT = 4    /* one dot product (chunk) per workgroup */
+} lg_plan_kernel;
 
 /* Operand load modes of the tiled kernel. */
 typedef enum lg_load_mode {
@@ -389,10 +399,13 @@ typedef struct lg_contract_plan {
     uint64_t k_chunk;     /* K elements per split */
     uint64_t workgroups;  /* workgroups of the main launch */
     uint64_t scratch_bytes; /* device scratch of the split-K partials */
-    uint32_t tile_m;      /* output tile of one workgroup (tiled/split): 128x128; 64x64 when */
-    uint32_t tile_n;      /* 128x128 tiles would leave most compute units idle; 32x32 (one
-                             launch, sixteen waves splitting K) for small outputs with
-                             K <= 1024; f16: 64x64 */
+    uint32_t tile_m;      /* output tile of one workgroup or wave (tiled/split): 128x128; */
+    uint32_t tile_n;      /* 64x64 when 128x128 tiles would leave most compute units idle or
+                             be mostly padding; 32x32 for small outputs (sixteen waves per tile
+                             splitting K) and batches of small products (one tile per wave);
+                             1x1 for dot products; f16: 64x64 */
+    uint32_t kernel;      /* lg_plan_kernel */
+    uint32_t swapped;     /* 1 when C is contiguous along M and is computed as C^T = B^T.A^T */
 } lg_contract_plan;
 
 lg_status lg_plan_contract_f32(float alpha, const lg_view* a, const char* a_labels,

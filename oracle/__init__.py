@@ -96,11 +96,21 @@ def gemm_seq(m, n, k, alpha, beta, a, a_off, a_strides, b, b_off, b_strides, c, 
                               c_strides[0], c_strides[1])
 
 
+def default_threads() -> int:
+    """Threads for the threaded forms: the CPUs this process may run on, at most 16 (the
+    CPU share of one GPU on the GPU hosts, whatever their total count)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
 def gemm_fast(m, n, k, alpha, beta, a, a_off, a_strides, b, b_off, b_strides, c, c_off,
               c_strides, rows=None, threads=None):
     """Bit-identical multi-threaded form; `rows` restricts the computed rows."""
     if threads is None:
-        threads = os.cpu_count() or 1
+        threads = default_threads()
     rp = None
     nrows = 0
     if rows is not None:
@@ -133,7 +143,7 @@ def gather_words_mt(words: np.ndarray, w: int, offset: int, shape, strides, conj
                     complex_elem=False, threads=None) -> np.ndarray:
     """gather_words with the logical elements split into `threads` contiguous ranges."""
     if threads is None:
-        threads = os.cpu_count() or 1
+        threads = default_threads()
     words = np.ascontiguousarray(words, dtype=np.uint32)
     n = int(np.prod(shape, dtype=np.uint64)) if len(shape) else 1
     out = np.zeros(max(n * w, 1), dtype=np.uint32)

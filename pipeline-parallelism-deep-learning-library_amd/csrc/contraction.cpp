@@ -397,6 +397,7 @@ struct Plan {
     bool half = false;  // f16 operands: the h* argument blocks below are the live ones
     GemmArgs gemm{};
     ReduceArgs reduce{};
+    DotArgs dot{};
     GeneralArgs general{};
     FillArgs fill{};
     GemmHalfArgs hgemm{};
@@ -499,20 +500,63 @@ void plan_half(const View& a, const View& b, const View& c, const Merged& mg, fl
     info.workgroups = wg;
 }
 
-// (splits, k_chunk): one split when the output already fills the chip or K is short.
-void split_shape(uint64_t tiles, uint32_t k, uint32_t* splits, uint32_t* chunk) {
+// (splits, k_chunk): one split when the output already fills the chip or K is short. The split
+// count is capped so the partials (split_bytes each) fit in SPLIT_PARTIAL_MAX.
+void split_shape(uint64_t tiles, uint32_t k, uint64_t split_bytes, uint32_t* splits,
+                 uint32_t* chunk) {
     *splits = 1;
     *chunk = k;
     if (tiles >= SPLIT_TARGET / 2 || k < 2 * SPLIT_MIN_CHUNK) return;
     const uint64_t want = (SPLIT_TARGET + tiles - 1) / tiles;
     const uint64_t by_k = k / SPLIT_MIN_CHUNK;
-    const uint64_t rough = std::max<uint64_t>(1, std::min<uint64_t>({want, by_k, SPLIT_MAX}));
+    const uint64_t by_room = SPLIT_PARTIAL_MAX / split_bytes;
+    const uint64_t rough = std::max<uint64_t>(1, std::min<uint64_t>({want, by_k, SPLIT_MAX, by_room}));
     uint64_t c = (k + rough - 1) / rough;
     c = (c + GEMM_BK - 1) / GEMM_BK * GEMM_BK;
     if (c == 0 || c >= k) return;
     *chunk = static_cast<uint32_t>(c);
     *splits = static_cast<uint32_t>((k + c - 1) / c);
 }
+
+// The same for 32x32 tiles of sixteen waves (gemm_f32_small): each split at least
+// SMALL_SPLIT_CHUNK deep (one full batch of loads for every wave), SMALL_SPLIT_TARGET
+// workgroups in all (two per compute unit: each holds 64 KB of LDS).
+constexpr uint32_t SMALL_SPLIT_CHUNK = 512;
+constexpr uint32_t SMALL_SPLIT_TARGET = 512;
+void small_split_shape(uint64_t tiles, uint32_t k, uint64_t split_bytes, uint32_t* splits,
+                       uint32_t* chunk) {
+    *splits = 1;
+    *chunk = k;
+    if (tiles >= SMALL_SPLIT_TARGET / 2 || k < 2 * SMALL_SPLIT_CHUNK) return;
+    const uint64_t want = (SMALL_SPLIT_TARGET + tiles - 1) / tiles;
+    const uint64_t rough = std::max<uint64_t>(
+        1, std::min<uint64_t>({want, k / SMALL_SPLIT_CHUNK, SPLIT_MAX, SPLIT_PARTIAL_MAX / split_bytes}));
+    uint64_t c = (k + rough - 1) / rough;
+    c = (c + SMALL_SPLIT_CHUNK - 1) / SMALL_SPLIT_CHUNK * SMALL_SPLIT_CHUNK;
+    if (c >= k) return;
+    *chunk = static_cast<uint32_t>(c);
+    *splits = static_cast<uint32_t>((k + c - 1) / c);
+}
+
+// The dot path's split: DOT_TARGET workgroups in all, each chunk at least DOT_MIN_CHUNK and a
+// multiple of 1024 (four elements for each of 256 threads), at most TICKET_WORDS products.
+void dot_split_shape(uint32_t batch, uint32_t k, uint32_t* splits, uint32_t* chunk) {
+    *splits = 1;
+    *chunk = k;
+    if (batch >= DOT_TARGET / 2 || batch > TICKET_WORDS || k < 2 * DOT_MIN_CHUNK) return;
+    const uint64_t want = (DOT_TARGET + batch - 1) / batch;
+    const uint64_t rough = std::max<uint64_t>(
+        1, std::min<uint64_t>({want, k / DOT_MIN_CHUNK, SPLIT_PARTIAL_MAX / (4ull * batch)}));
+    uint64_t c = (k + rough - 1) / rough;
+    c = (c + 1023) / 1024 * 1024;
+    if (c >= k) return;
+    *chunk = static_cast<uint32_t>(c);
+    *splits = static_cast<uint32_t>((k + c - 1) / c);
+}
+
+// Waves a many-tile 32x32 product needs before it takes one tile per wave (gemm_f32_wave)
+// rather than sixteen waves per tile (gemm_f32_small).
+constexpr uint64_t WAVE_MIN_TILES = 1024;
 
 // 128-bit loads need the view's first element 16-byte aligned (allocation base included) and
 // every other stride a multiple of four elements.
@@ -596,72 +640,147 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
         return p;
     }
     const Axis &ab = mg.batch[0], &am = mg.m[0], &an = mg.n[0], &ak = mg.k[0];
+    if (m == 1 && n == 1) {
+        // Dot products: memory-bound, summed on the VALU.
+        DotArgs& d = p.dot;
+        d.a = aptr;
+        d.b = bptr;
+        d.c = cptr;
+        d.a_sb = sfit(ab.a, "A batch stride");
+        d.a_sk = sfit(ak.a, "A K stride");
+        d.b_sb = sfit(ab.b, "B batch stride");
+        d.b_sk = sfit(ak.b, "B K stride");
+        d.c_sb = sfit(ab.c, "C batch stride");
+        d.k = k;
+        d.batch = batch;
+        d.alpha = alpha;
+        d.beta = beta;
+        d.scale_b = 0;
+        uint32_t splits = 1, chunk = k;
+        dot_split_shape(batch, k, &splits, &chunk);
+        if (static_cast<uint64_t>(batch) * splits > 0x7fffffffull) {
+            fail_invalid("problem exceeds one launch's workgroup count");
+        }
+        d.splits = splits;
+        d.k_chunk = chunk;
+        const bool vec = ak.a == 1 && ak.b == 1 && ab.a % 4 == 0 && ab.b % 4 == 0 &&
+                         (a.base + a.offset * sizeof(float)) % 16 == 0 &&
+                         (b.base + b.offset * sizeof(float)) % 16 == 0;
+        info.kind = LG_PLAN_DOT;
+        info.kernel = LG_KERNEL_DOT;
+        info.a_mode = info.b_mode = vec ? LG_LOAD_K_CONTIG : LG_LOAD_STRIDED;
+        info.tile_m = info.tile_n = 1;
+        info.splits = splits;
+        info.k_chunk = chunk;
+        info.workgroups = static_cast<uint64_t>(batch) * splits;
+        info.scratch_bytes = splits > 1 ? static_cast<uint64_t>(batch) * splits * sizeof(float) : 0;
+        return p;
+    }
+    // Operand roles. C contiguous along M (and not along N) is computed as C^T = B^T.A^T, so
+    // the epilogue's stores run along C's unit stride; alpha then multiplies the operand loaded
+    // as B (the caller's A), and every product is still (alpha*a)*b.
+    struct Role {
+        const float* ptr;
+        uintptr_t base;
+        uint64_t offset, sb, srow, sk;
+    };
+    Role ra{aptr, a.base, a.offset, ab.a, am.a, ak.a};
+    Role rb{bptr, b.base, b.offset, ab.b, an.b, ak.b};
+    uint64_t c_sm = am.c, c_sn = an.c;
+    const bool swap = am.c == 1 && an.c != 1;
+    uint32_t mm = m, nn = n;
+    if (swap) {
+        std::swap(ra, rb);
+        std::swap(c_sm, c_sn);
+        std::swap(mm, nn);
+    }
+    info.swapped = swap ? 1 : 0;
     GemmArgs& t = p.gemm;
-    t.a = aptr;
-    t.b = bptr;
+    t.a = ra.ptr;
+    t.b = rb.ptr;
     t.c = cptr;
     t.partial = nullptr;
-    t.a_sb = sfit(ab.a, "A batch stride");
-    t.a_sm = sfit(am.a, "A M stride");
-    t.a_sk = sfit(ak.a, "A K stride");
-    t.b_sb = sfit(ab.b, "B batch stride");
-    t.b_sn = sfit(an.b, "B N stride");
-    t.b_sk = sfit(ak.b, "B K stride");
+    t.a_sb = sfit(ra.sb, "A batch stride");
+    t.a_sm = sfit(ra.srow, "A M stride");
+    t.a_sk = sfit(ra.sk, "A K stride");
+    t.b_sb = sfit(rb.sb, "B batch stride");
+    t.b_sn = sfit(rb.srow, "B N stride");
+    t.b_sk = sfit(rb.sk, "B K stride");
     t.c_sb = sfit(ab.c, "C batch stride");
-    t.c_sm = sfit(am.c, "C M stride");
-    t.c_sn = sfit(an.c, "C N stride");
-    t.m = m;
-    t.n = n;
+    t.c_sm = sfit(c_sm, "C M stride");
+    t.c_sn = sfit(c_sn, "C N stride");
+    t.m = mm;
+    t.n = nn;
     t.k = k;
     t.batch = batch;
     t.alpha = alpha;
     t.beta = beta;
-    // 128x128 tiles load half the operand bytes per product of 64x64 ones, so they are kept
-    // whenever their grid, split along K as far as split_shape would go, reaches
-    // GEMM_SMALL_BELOW workgroups; otherwise 64x64 tiles give four times the workgroups
-    // before split-K adds more.
-    const uint64_t big = static_cast<uint64_t>((m + GEMM_BM - 1) / GEMM_BM) *
-                         ((n + GEMM_BN - 1) / GEMM_BN) * batch;
+    t.scale_b = swap ? 1 : 0;
+    // Tile choice. 128x128 tiles load half the operand bytes per product of 64x64 ones, so they
+    // are kept whenever at least half of their area is output and their grid, split along K as
+    // far as split_shape would go, reaches GEMM_SMALL_BELOW workgroups; otherwise 64x64 tiles
+    // give four times the workgroups before split-K adds more. Outputs that even 64x64 tiles
+    // would pad past half (batches of small matrices, skinny outputs) take 32x32 tiles: one per
+    // wave when there are enough of them, else sixteen waves per tile splitting K.
+    auto grid_of = [&](uint32_t e) {
+        return static_cast<uint64_t>((mm + e - 1) / e) * ((nn + e - 1) / e) * batch;
+    };
+    const uint64_t useful = static_cast<uint64_t>(mm) * nn * batch;
+    const uint64_t big = grid_of(GEMM_BM), mid = grid_of(GEMM_SMALL_TILE), tiny = grid_of(GEMM_TINY_TILE);
     const uint64_t k_ways = std::max<uint64_t>(1, std::min<uint64_t>(k / SPLIT_MIN_CHUNK, SPLIT_MAX));
-    const uint64_t mid = static_cast<uint64_t>((m + GEMM_SMALL_TILE - 1) / GEMM_SMALL_TILE) *
-                         ((n + GEMM_SMALL_TILE - 1) / GEMM_SMALL_TILE) * batch;
     if (mid < GEMM_SMALL_BELOW && k <= GEMM_SMALL_K) {
         t.tile = GEMM_TINY_TILE;  // one launch, no split-K partials
-    } else {
+        t.kernel = KERN_SMALL;
+    } else if (2 * useful >= big * GEMM_BM * GEMM_BN) {
         t.tile = big * k_ways < GEMM_SMALL_BELOW ? GEMM_SMALL_TILE : GEMM_BM;
+        t.kernel = KERN_TILE;
+    } else if (2 * useful >= mid * GEMM_SMALL_TILE * GEMM_SMALL_TILE) {
+        t.tile = GEMM_SMALL_TILE;
+        t.kernel = KERN_TILE;
+    } else {
+        t.tile = GEMM_TINY_TILE;
+        t.kernel = tiny >= WAVE_MIN_TILES ? KERN_WAVE : KERN_SMALL;
     }
-    t.tiles_m = (m + t.tile - 1) / t.tile;
-    t.tiles_n = (n + t.tile - 1) / t.tile;
+    t.tiles_m = (mm + t.tile - 1) / t.tile;
+    t.tiles_n = (nn + t.tile - 1) / t.tile;
     info.tile_m = info.tile_n = t.tile;
-    const int a_mode = load_mode(a.base, a.offset, ab.a, am.a, ak.a);
-    const int b_mode = load_mode(b.base, b.offset, ab.b, an.b, ak.b);
+    info.kernel = t.kernel == KERN_TILE ? LG_KERNEL_TILE
+                  : t.kernel == KERN_SMALL ? LG_KERNEL_SMALL : LG_KERNEL_WAVE;
+    const int a_mode = load_mode(ra.base, ra.offset, ra.sb, ra.srow, ra.sk);
+    const int b_mode = load_mode(rb.base, rb.offset, rb.sb, rb.srow, rb.sk);
     info.a_mode = static_cast<uint32_t>(a_mode);
     info.b_mode = static_cast<uint32_t>(b_mode);
     const uint64_t tiles = static_cast<uint64_t>(t.tiles_m) * t.tiles_n * batch;
+    const uint64_t split_bytes = static_cast<uint64_t>(batch) * mm * nn * sizeof(float);
     uint32_t splits = 1, chunk = k;
-    if (t.tile != GEMM_TINY_TILE) split_shape(tiles, k, &splits, &chunk);
+    if (t.kernel == KERN_TILE) {
+        split_shape(tiles, k, split_bytes, &splits, &chunk);
+    } else if (t.kernel == KERN_SMALL && !(mid < GEMM_SMALL_BELOW && k <= GEMM_SMALL_K)) {
+        small_split_shape(tiles, k, split_bytes, &splits, &chunk);
+    }
     if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
     t.splits = splits;
     t.k_chunk = chunk;
     info.splits = splits;
     info.k_chunk = chunk;
-    info.workgroups = gemm_workgroups(m, n, batch, splits, t.tile);
+    info.workgroups = gemm_workgroups(t);
     if (splits == 1) {
         info.kind = LG_PLAN_TILED;
         return p;
     }
     info.kind = LG_PLAN_SPLIT;
-    info.scratch_bytes = static_cast<uint64_t>(splits) * batch * m * n * sizeof(float);
+    info.scratch_bytes = static_cast<uint64_t>(splits) * split_bytes;
     ReduceArgs& r = p.reduce;
     r.c = cptr;
     r.c_sb = t.c_sb;
     r.c_sm = t.c_sm;
     r.c_sn = t.c_sn;
-    r.m = m;
-    r.n = n;
+    r.m = mm;
+    r.n = nn;
     r.batch = batch;
     r.splits = splits;
     r.beta = beta;
+    r.slices = useful < 65536 && splits >= 64 ? 16 : 4;
     return p;
 }
 
@@ -695,41 +814,25 @@ Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, 
     return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta, half);
 }
 
-// The context's split-K buffer, at least `bytes` long, ordered after every earlier use.
-// Called with ctx->split_lock held.
-float* split_scratch(lg_ctx* ctx, hipStream_t s, uint64_t bytes) {
-    if (ctx->split_event == nullptr) {
-        check_hip(hipEventCreateWithFlags(&ctx->split_event, hipEventDisableTiming),
-                  "hipEventCreateWithFlags");
-    }
-    // Back-to-back calls on the context's own stream are ordered by it. Any other pair waits
-    // on the event, also when both are one caller's stream handle: the handle may name a new
-    // stream created after the old one was destroyed with work still queued.
-    const bool own = s == ctx->stream && ctx->split_stream == ctx->stream;
-    if (ctx->split_stream != nullptr && !own) {
-        if (ctx->split_stream == ctx->stream) {
-            check_hip(hipEventRecord(ctx->split_event, ctx->stream), "hipEventRecord");
-        }
-        check_hip(hipStreamWaitEvent(s, ctx->split_event, 0), "hipStreamWaitEvent");
-    }
-    if (bytes > ctx->split_bytes) {
-        if (ctx->split_scratch != nullptr) {
-            // `s` is now ordered after every use of the old buffer; let them finish first.
-            check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
-            check_hip(hipFree(ctx->split_scratch), "hipFree");
-            ctx->split_scratch = nullptr;
-            ctx->split_bytes = 0;
-        }
-        void* p = nullptr;
-        check_hip(hipMalloc(&p, bytes), "hipMalloc");
-        ctx->split_scratch = p;
-        ctx->split_bytes = bytes;
-    }
-    ctx->split_stream = s;
-    return static_cast<float*>(ctx->split_scratch);
+// Device scratch handed to a split or split-dot plan's launches: ticket words (zero between
+// calls) and the partials.
+struct Scratch {
+    float* partial = nullptr;
+    uint32_t* tickets = nullptr;
+};
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    check_hip(hipStreamIsCapturing(s, &st), "hipStreamIsCapturing");
+    return st != hipStreamCaptureStatusNone;
 }
 
-void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
+bool needs_scratch(const Plan& p) {
+    return !p.half && (p.info.kind == LG_PLAN_SPLIT || (p.info.kind == LG_PLAN_DOT && p.dot.splits > 1));
+}
+
+// Enqueues the plan's launches; split and split-dot plans use `sc`.
+void launch_plan(lg_ctx* ctx, hipStream_t s, Plan& p, const Scratch& sc) {
     if (p.half) {
         switch (p.info.kind) {
             case LG_PLAN_ZERO:
@@ -761,20 +864,54 @@ void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
             launch_gemm(ctx, s, p.gemm, static_cast<int>(p.info.a_mode),
                         static_cast<int>(p.info.b_mode));
             return;
-        case LG_PLAN_SPLIT: {
-            std::lock_guard<std::mutex> hold(ctx->split_lock);
-            float* partial = split_scratch(ctx, s, p.info.scratch_bytes);
-            p.gemm.partial = partial;
-            p.reduce.partial = partial;
+        case LG_PLAN_SPLIT:
+            p.gemm.partial = sc.partial;
+            p.reduce.partial = sc.partial;
             launch_gemm(ctx, s, p.gemm, static_cast<int>(p.info.a_mode),
                         static_cast<int>(p.info.b_mode));
             launch_reduce(ctx, s, p.reduce);
-            if (s != ctx->stream) {
-                // Marks the end of this use for a later call on another stream; the context's
-                // own stream outlives the buffer, so its uses are marked only when needed.
-                check_hip(hipEventRecord(ctx->split_event, s), "hipEventRecord");
-            }
             return;
+        case LG_PLAN_DOT:
+            p.dot.partial = sc.partial;
+            p.dot.tickets = sc.tickets;
+            launch_dot(ctx, s, p.dot, p.info.a_mode == LG_LOAD_K_CONTIG);
+            return;
+    }
+}
+
+void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
+    if (!needs_scratch(p)) {
+        launch_plan(ctx, s, p, Scratch{});
+        return;
+    }
+    // The context's scratch, made with the context and never grown, so this path allocates
+    // nothing and never blocks. Eager calls are ordered after the previous user: calls on the
+    // context's own stream by the stream, any other pair by split_event (also when both are
+    // one caller's stream handle: the handle may name a new stream created after the old one
+    // was destroyed with work still queued). A call under stream capture cannot wait on or
+    // record an eager event; it is ordered only by its own stream, so replays of the graph
+    // must not overlap the context's other split work (the caller orders them).
+    std::lock_guard<std::mutex> hold(ctx->split_lock);
+    const bool cap = capturing(s);
+    if (!cap) {
+        const bool own = s == ctx->stream && ctx->split_stream == ctx->stream;
+        if (ctx->split_stream != nullptr && !own) {
+            if (ctx->split_stream == ctx->stream) {
+                check_hip(hipEventRecord(ctx->split_event, ctx->stream), "hipEventRecord");
+            }
+            check_hip(hipStreamWaitEvent(s, ctx->split_event, 0), "hipStreamWaitEvent");
+        }
+    }
+    Scratch sc;
+    sc.tickets = static_cast<uint32_t*>(ctx->split_scratch);
+    sc.partial = reinterpret_cast<float*>(static_cast<char*>(ctx->split_scratch) + TICKET_BYTES);
+    launch_plan(ctx, s, p, sc);
+    if (!cap) {
+        ctx->split_stream = s;
+        if (s != ctx->stream) {
+            // Marks the end of this use for a later call on another stream; the context's own
+            // stream outlives the buffer, so its uses are marked only when needed.
+            check_hip(hipEventRecord(ctx->split_event, s), "hipEventRecord");
         }
     }
 }
@@ -787,6 +924,26 @@ void run(lg_ctx* ctx, void* stream, Plan plan, bool wait) {
 }
 
 }  // namespace
+
+void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                const lg_view* b, float beta, const lg_view* c,
+                                uint64_t partial_cap, uint32_t* (*scratch)(lg_ctx*, hipStream_t)) {
+    View va, vb, vc;
+    Plan plan = plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc);
+    if (plan.info.scratch_bytes > partial_cap) {
+        fail_invalid("product needs " + std::to_string(plan.info.scratch_bytes) +
+                     " bytes of split scratch; at most " + std::to_string(partial_cap) +
+                     " are available");
+    }
+    set_device(ctx);
+    hipStream_t s = pick_stream(ctx, stream);
+    Scratch sc;
+    if (needs_scratch(plan)) {
+        sc.tickets = scratch(ctx, s);
+        sc.partial = reinterpret_cast<float*>(sc.tickets + TICKET_WORDS);
+    }
+    launch_plan(ctx, s, plan, sc);
+}
 
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
                         float beta, const View& c, uint32_t dtype) {

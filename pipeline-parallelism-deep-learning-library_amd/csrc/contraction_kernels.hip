@@ -1,6 +1,7 @@
-// gfx950 contraction kernels: the fp32 MFMA GEMM (gemm_kernel.h) instantiated at the
-// library's pipeline shape, the split-K reduction (fixed order over splits, so results are
-// bit-reproducible), the mixed-radix general fallback, and the C = 0 / C = beta*C fill.
+// gfx950 contraction kernels: the fp32 MFMA GEMM kernels (gemm_kernel.h) instantiated at the
+// library's pipeline shapes, the split-K reduction (fixed order over splits, so results are
+// bit-reproducible), dot products, the mixed-radix general fallback, and the C = 0 /
+// C = beta*C fill.
 // Every product is formed as (alpha * a) * b, the grouping of the reference's sequential loop.
 // Everything is compiled with -ffp-contract=off: products and sums round separately.
 #include <hip/hip_runtime.h>
@@ -13,26 +14,29 @@ namespace {
 
 using gemm_detail::gemm_f32_mfma;
 using gemm_detail::gemm_f32_small;
+using gemm_detail::gemm_f32_wave;
 using gemm_detail::SMALL_WAVES;
+using gemm_detail::WAVE_TILES;
 
 // Split-K second pass. Partials are [batch][splits][m][n], dense. A workgroup owns 64 runs
-// of V consecutive outputs; its four waves each sum a fixed quarter of the splits in
-// ascending order (8 loads in flight), the quarters are added in order 0+1+2+3, and beta*C
-// is added once (alpha is already inside the partials). The order depends only on the split
-// count, so results are
-// bit-reproducible from run to run. V = 4 (128-bit loads) whenever n is a multiple of 4.
+// of V consecutive outputs; its SL waves each sum a fixed 1/SL of the splits in ascending
+// order (8 loads in flight), the slices are added in order 0+1+...+(SL-1), and beta*C is added
+// once (alpha is already inside the partials). The order depends only on the split count and
+// SL (the planner picks SL from the shape), so results are bit-reproducible from run to run.
+// V = 4 (128-bit loads) whenever n is a multiple of 4. SL = 16 serves few outputs with many
+// splits (the small-output split path), where four waves per output run would leave the
+// loads of one output's splits mostly in series.
 constexpr int RED_LANES = 64;
-constexpr int RED_SLICES = 4;
 
-template <int V>
-__global__ __launch_bounds__(RED_LANES * RED_SLICES) void reduce_f32(ReduceArgs p) {
+template <int V, int SL>
+__global__ __launch_bounds__(RED_LANES * SL) void reduce_f32(ReduceArgs p) {
     typedef float vec __attribute__((ext_vector_type(4)));
-    __shared__ vec part[RED_SLICES][RED_LANES];
+    __shared__ vec part[SL][RED_LANES];
     const int lane = threadIdx.x % RED_LANES, q = threadIdx.x / RED_LANES;
     const uint64_t mn = static_cast<uint64_t>(p.m) * p.n;
     const uint64_t count = mn * p.batch;
-    const uint32_t s0 = static_cast<uint32_t>(static_cast<uint64_t>(q) * p.splits / RED_SLICES);
-    const uint32_t s1 = static_cast<uint32_t>(static_cast<uint64_t>(q + 1) * p.splits / RED_SLICES);
+    const uint32_t s0 = static_cast<uint32_t>(static_cast<uint64_t>(q) * p.splits / SL);
+    const uint32_t s1 = static_cast<uint32_t>(static_cast<uint64_t>(q + 1) * p.splits / SL);
     const uint64_t step = static_cast<uint64_t>(gridDim.x) * RED_LANES * V;
     for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * RED_LANES * V; base < count; base += step) {
         const uint64_t e = base + static_cast<uint64_t>(lane) * V;
@@ -69,7 +73,7 @@ __global__ __launch_bounds__(RED_LANES * RED_SLICES) void reduce_f32(ReduceArgs 
         if (q == 0 && e < count) {
             vec t = part[0][lane];
 #pragma unroll
-            for (int k = 1; k < RED_SLICES; ++k) t = t + part[k][lane];
+            for (int k = 1; k < SL; ++k) t = t + part[k][lane];
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 const uint64_t r = rem + v;
@@ -82,6 +86,111 @@ __global__ __launch_bounds__(RED_LANES * RED_SLICES) void reduce_f32(ReduceArgs 
             }
         }
         __syncthreads();
+    }
+}
+
+// Dot products, C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k] (M = N = 1, memory-bound:
+// 8 bytes per multiply-add, so the VALU rather than a mostly-padded MFMA tile). Workgroup
+// (b, s) takes K chunk s of product b; thread t sums the elements t, t + 256, ... of the chunk
+// (128-bit runs of 4 when VEC) in index order, and the workgroup adds the 256 thread sums in a
+// fixed tree. With one split that is the result; otherwise it is partial[b][s], and the
+// workgroup that draws the last ticket of product b (a device-scope counter; every partial is
+// released before its ticket is drawn) adds the partials: thread t sums splits t, t + 256, ...
+// in order, then the same tree. It then returns the ticket word to zero for the next call on
+// the scratch. The order depends only on K, the chunk and the split count. Nothing waits on
+// another workgroup, so no schedule can hang.
+constexpr int DOT_UNROLL = 4;  // 128-bit runs whose loads are issued before their products
+
+__device__ inline float dot_tree(float* red, float v) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+#pragma unroll
+    for (int w = DOT_THREADS / 2; w > 0; w /= 2) {
+        if (static_cast<int>(threadIdx.x) < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    return red[0];
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(DOT_THREADS) void dot_f32(DotArgs p) {
+    typedef float vec __attribute__((ext_vector_type(4)));
+    __shared__ float red[DOT_THREADS];
+    __shared__ bool last;
+    const uint32_t bi = blockIdx.x / p.splits, split = blockIdx.x - bi * p.splits;
+    const uint32_t kb = split * p.k_chunk;
+    const uint32_t klen = min(p.k - kb, p.k_chunk);
+    const float* a = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(kb) * p.a_sk;
+    const float* b = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(kb) * p.b_sk;
+    const float alpha_a = p.scale_b ? 1.0f : p.alpha, alpha_b = p.scale_b ? p.alpha : 1.0f;
+    float acc = 0.0f;
+    auto add = [&](float x, float y) {
+        if (alpha_a != 1.0f) x = alpha_a * x;
+        if (alpha_b != 1.0f) y = alpha_b * y;
+        acc = acc + x * y;
+    };
+    uint32_t i = threadIdx.x;
+    if constexpr (VEC) {
+        // klen is a multiple of 4 except in the last chunk, whose tail the scalar loop takes.
+        const vec* av = reinterpret_cast<const vec*>(a);
+        const vec* bv = reinterpret_cast<const vec*>(b);
+        const uint32_t nv = klen / 4;
+        for (; i + (DOT_UNROLL - 1) * DOT_THREADS < nv; i += DOT_UNROLL * DOT_THREADS) {
+            vec x[DOT_UNROLL], y[DOT_UNROLL];
+#pragma unroll
+            for (int u = 0; u < DOT_UNROLL; ++u) {
+                x[u] = av[i + u * DOT_THREADS];
+                y[u] = bv[i + u * DOT_THREADS];
+            }
+#pragma unroll
+            for (int u = 0; u < DOT_UNROLL; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) add(x[u][e], y[u][e]);
+        }
+        for (; i < nv; i += DOT_THREADS) {
+            const vec x = av[i], y = bv[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) add(x[e], y[e]);
+        }
+        // The chunk's last klen % 4 elements go to the threads after the vector runs.
+        i = nv * 4 + threadIdx.x;
+        if (i < klen) add(a[i], b[i]);
+    } else {
+        for (; i < klen; i += DOT_THREADS) {
+            add(a[static_cast<int64_t>(i) * p.a_sk], b[static_cast<int64_t>(i) * p.b_sk]);
+        }
+    }
+    const float sum = dot_tree(red, acc);
+    float* c = p.c + static_cast<int64_t>(bi) * p.c_sb;
+    if (p.splits == 1) {
+        if (threadIdx.x == 0) *c = p.beta != 0.0f ? p.beta * *c + sum : sum;
+        return;
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(p.partial + blockIdx.x, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        last = __hip_atomic_fetch_add(p.tickets + bi, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+               p.splits - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float t = 0.0f;
+    for (uint32_t g = threadIdx.x; g < p.splits; g += DOT_THREADS) {
+        t = t + __hip_atomic_load(p.partial + static_cast<uint64_t>(bi) * p.splits + g, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const float total = dot_tree(red, t);
+    if (threadIdx.x == 0) {
+        *c = p.beta != 0.0f ? p.beta * *c + total : total;
+        __hip_atomic_store(p.tickets + bi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__global__ __launch_bounds__(256) void clear_words(uint32_t* p, uint64_t words) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        p[i] = 0u;
     }
 }
 
@@ -151,7 +260,9 @@ void check_launch(const char* what) { check_hip(hipGetLastError(), what); }
 
 template <int AM, int BMD>
 void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
-    if (a.tile == GEMM_TINY_TILE) {
+    if (a.kernel == KERN_WAVE) {
+        hipLaunchKernelGGL((gemm_f32_wave<AM, BMD>), dim3(groups), dim3(64 * WAVE_TILES), 0, s, a);
+    } else if (a.kernel == KERN_SMALL) {
         hipLaunchKernelGGL((gemm_f32_small<AM, BMD, SMALL_WAVES>), dim3(groups), dim3(64 * SMALL_WAVES), 0,
                            s, a);
     } else if (a.tile == GEMM_SMALL_TILE) {
@@ -167,18 +278,25 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
 
 }  // namespace
 
-uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits, uint32_t tile) {
-    const uint64_t tm = (m + tile - 1) / tile, tn = (n + tile - 1) / tile;
-    return tm * tn * batch * splits;
+uint64_t gemm_workgroups(const GemmArgs& a) {
+    const uint64_t tiles = static_cast<uint64_t>((a.m + a.tile - 1) / a.tile) *
+                           ((a.n + a.tile - 1) / a.tile) * a.batch * a.splits;
+    return a.kernel == KERN_WAVE ? (tiles + WAVE_TILES - 1) / WAVE_TILES : tiles;
 }
 
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode) {
-    const uint32_t groups =
-        static_cast<uint32_t>(gemm_workgroups(args.m, args.n, args.batch, args.splits, args.tile));
-    static const char* const names[3][3] = {
-        {"gemm_f32_mfma<K,K>", "gemm_f32_mfma<K,MN>", "gemm_f32_mfma<K,S>"},
-        {"gemm_f32_mfma<MN,K>", "gemm_f32_mfma<MN,MN>", "gemm_f32_mfma<MN,S>"},
-        {"gemm_f32_mfma<S,K>", "gemm_f32_mfma<S,MN>", "gemm_f32_mfma<S,S>"}};
+    const uint32_t groups = static_cast<uint32_t>(gemm_workgroups(args));
+    static const char* const names[3][3][3] = {
+        {{"gemm_f32_mfma<K,K>", "gemm_f32_mfma<K,MN>", "gemm_f32_mfma<K,S>"},
+         {"gemm_f32_mfma<MN,K>", "gemm_f32_mfma<MN,MN>", "gemm_f32_mfma<MN,S>"},
+         {"gemm_f32_mfma<S,K>", "gemm_f32_mfma<S,MN>", "gemm_f32_mfma<S,S>"}},
+        {{"gemm_f32_small<K,K>", "gemm_f32_small<K,MN>", "gemm_f32_small<K,S>"},
+         {"gemm_f32_small<MN,K>", "gemm_f32_small<MN,MN>", "gemm_f32_small<MN,S>"},
+         {"gemm_f32_small<S,K>", "gemm_f32_small<S,MN>", "gemm_f32_small<S,S>"}},
+        {{"gemm_f32_wave<K,K>", "gemm_f32_wave<K,MN>", "gemm_f32_wave<K,S>"},
+         {"gemm_f32_wave<MN,K>", "gemm_f32_wave<MN,MN>", "gemm_f32_wave<MN,S>"},
+         {"gemm_f32_wave<S,K>", "gemm_f32_wave<S,MN>", "gemm_f32_wave<S,S>"}}};
+    if (args.kernel > KERN_WAVE) fail_invalid("unknown GEMM kernel");
 #define LG_GEMM_CASE(AMV, BMV)                       \
     if (a_mode == AMV && b_mode == BMV) {            \
         launch_gemm_t<AMV, BMV>(s, args, groups);    \
@@ -193,8 +311,8 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
     LG_GEMM_CASE(LOAD_S, LOAD_MN)
     LG_GEMM_CASE(LOAD_S, LOAD_S) { fail_invalid("unknown operand load mode"); }
 #undef LG_GEMM_CASE
-    check_launch("gemm_f32_mfma launch");
-    note_launch(ctx, names[a_mode][b_mode]);
+    check_launch("gemm launch");
+    note_launch(ctx, names[args.kernel][a_mode][b_mode]);
 }
 
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args) {
@@ -203,13 +321,40 @@ void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args) {
     const uint64_t per = static_cast<uint64_t>(RED_LANES) * v;
     const uint64_t g = (count + per - 1) / per;
     const dim3 grid(static_cast<uint32_t>(g < 65536 ? (g ? g : 1) : 65536));
-    if (v == 4) {
-        hipLaunchKernelGGL(reduce_f32<4>, grid, dim3(RED_LANES * RED_SLICES), 0, s, args);
+    if (args.slices == 16) {
+        if (v == 4) {
+            hipLaunchKernelGGL((reduce_f32<4, 16>), grid, dim3(RED_LANES * 16), 0, s, args);
+        } else {
+            hipLaunchKernelGGL((reduce_f32<1, 16>), grid, dim3(RED_LANES * 16), 0, s, args);
+        }
+    } else if (args.slices == 4) {
+        if (v == 4) {
+            hipLaunchKernelGGL((reduce_f32<4, 4>), grid, dim3(RED_LANES * 4), 0, s, args);
+        } else {
+            hipLaunchKernelGGL((reduce_f32<1, 4>), grid, dim3(RED_LANES * 4), 0, s, args);
+        }
     } else {
-        hipLaunchKernelGGL(reduce_f32<1>, grid, dim3(RED_LANES * RED_SLICES), 0, s, args);
+        fail_invalid("reduction slices must be 4 or 16");
     }
     check_launch("reduce_f32 launch");
     note_launch(ctx, "reduce_f32");
+}
+
+void launch_dot(Context* ctx, hipStream_t s, const DotArgs& args, bool vec) {
+    const uint64_t groups = static_cast<uint64_t>(args.batch) * args.splits;
+    if (vec) {
+        hipLaunchKernelGGL(dot_f32<true>, dim3(static_cast<uint32_t>(groups)), dim3(DOT_THREADS), 0, s, args);
+    } else {
+        hipLaunchKernelGGL(dot_f32<false>, dim3(static_cast<uint32_t>(groups)), dim3(DOT_THREADS), 0, s, args);
+    }
+    check_launch("dot_f32 launch");
+    note_launch(ctx, "dot_f32");
+}
+
+void launch_clear_words(Context* ctx, hipStream_t s, uint32_t* p, uint64_t words) {
+    hipLaunchKernelGGL(clear_words, dim3(grid_for(words)), dim3(256), 0, s, p, words);
+    check_launch("clear_words launch");
+    note_launch(ctx, "clear_words");
 }
 
 void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args) {

@@ -123,8 +123,8 @@ __device__ inline const float* slice_ptr(const float* p, int64_t srow, int64_t s
     }
 }
 
-// Writes a loaded K-slice into its LDS stage. With SCALE (operand A) every element is first
-// multiplied by alpha, so each product the MFMAs form is (alpha*a)*b. alpha is finite here
+// Writes a loaded K-slice into its LDS stage. With SCALE every element is first multiplied by
+// alpha (unless alpha is 1), so each product the MFMAs form is (alpha*a)*b. alpha is finite here
 // (the planner sends non-finite alpha to the general kernel), so zero padding stays zero.
 template <int MODE, int BK, int R, bool SCALE, typename G = Geo<BK, R>>
 __device__ inline void store_slice(float* __restrict__ st, const floatx4 (&r)[G::LOADS],
@@ -255,9 +255,12 @@ void gemm_f32_mfma(GemmArgs p) {
             load_slice<BMD, false, BK, TBN>(rb, B, p.b_sn, p.b_sk, nrem, k0, klen, tid);
         }
     };
+    // alpha multiplies whichever operand holds the caller's A (1 * x is skipped as x).
+    const float alpha_a = p.scale_b ? 1.0f : p.alpha;
+    const float alpha_b = p.scale_b ? p.alpha : 1.0f;
     load(0);
-    store_slice<AM, BK, TBM, true>(As, ra, tid, p.alpha);
-    store_slice<BMD, BK, TBN, false>(Bs, rb, tid, 1.0f);
+    store_slice<AM, BK, TBM, true>(As, ra, tid, alpha_a);
+    store_slice<BMD, BK, TBN, true>(Bs, rb, tid, alpha_b);
     if constexpr (AHEAD) {
         if (ktiles > 1) load(BK);
     }
@@ -282,8 +285,8 @@ void gemm_f32_mfma(GemmArgs p) {
                     read_frag<BMD, BK, TBN, TN>(bv, bs, wn * 32 * TN, g, lr, h);
                     mfma_group<TM, TN>(acc, av, bv);
                     if (g == 0) {
-                        store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
-                        store_slice<BMD, BK, TBN, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);
+                        store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
+                        store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
                         const uint32_t k0 = (kt + 2) * BK;
                         const int64_t oa = AM == LOAD_MN ? static_cast<int64_t>(k0) * p.a_sk : k0;
                         const int64_t ob = BMD == LOAD_MN ? static_cast<int64_t>(k0) * p.b_sk : k0;
@@ -316,8 +319,8 @@ void gemm_f32_mfma(GemmArgs p) {
             if constexpr (AHEAD) {
                 if (g == 0) {
                     if (more) {
-                        store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
-                        store_slice<BMD, BK, TBN, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);
+                        store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
+                        store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
                     }
                     if (kt + 2 < ktiles) load((kt + 2) * BK);
                 }
@@ -326,8 +329,8 @@ void gemm_f32_mfma(GemmArgs p) {
         __builtin_amdgcn_s_setprio(0);
         if constexpr (!AHEAD) {
             if (more) {
-                store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, p.alpha);
-                store_slice<BMD, BK, TBN, false>(Bs + (s ^ 1) * B_ST, rb, tid, 1.0f);
+                store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
+                store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
             }
         }
         __syncthreads();
@@ -370,16 +373,18 @@ void gemm_f32_mfma(GemmArgs p) {
             }
 }
 
-// Small products (the 64x64 grid alone under 256 tiles, K <= GEMM_SMALL_K): one 32x32 output
-// tile per workgroup of W waves in a single launch. The waves take interleaved 8-k groups
-// (wave w: groups w, w+W, ...), each accumulating one v_mfma_f32_32x32x2_f32 block straight
-// from registers: the 32 rows are shared by the waves but their k ranges are not, so there is
-// nothing for LDS to reuse. Lane (r = lane%32, h = lane/32) holds k = 8g + 4h + s at MFMA
-// step s, as in the tiled kernel; an operand contiguous along K gives it a 128-bit load, one
-// contiguous along M/N four 32-bit loads that coalesce across lanes. The W wave sums meet in
-// LDS and add in wave order, then beta*C + sum: the order depends on K and W alone. The
-// launch uses W = 16 (four waves per SIMD): with K = 512 each wave issues all of its loads at
-// once and the SIMD interleaves four accumulation chains (config 1: 33 -> 38 TFLOP/s).
+// Small products (the 64x64 grid alone under 256 tiles, K <= GEMM_SMALL_K), and small
+// outputs with long K split over workgroups: one 32x32 output tile (of one K chunk) per
+// workgroup of W waves. The waves take interleaved 8-k groups (wave w: groups w, w+W, ...),
+// each accumulating one v_mfma_f32_32x32x2_f32 block straight from registers: the 32 rows are
+// shared by the waves but their k ranges are not, so there is nothing for LDS to reuse. Lane
+// (r = lane%32, h = lane/32) holds k = 8g + 4h + s at MFMA step s, as in the tiled kernel; an
+// operand contiguous along K gives it a 128-bit load, one contiguous along M/N four 32-bit
+// loads that coalesce across lanes. The W wave sums meet in LDS and add in wave order, then
+// beta*C + sum (or the raw sum into the split partials): the order depends on K, the chunk
+// and W alone. The launch uses W = 16 (four waves per SIMD): with K = 512 each wave issues
+// all of its loads at once and the SIMD interleaves four accumulation chains (config 1:
+// 33 -> 38 TFLOP/s).
 constexpr int SMALL_TILE = 32;
 constexpr int SMALL_WAVES = 16;  // waves per small-product workgroup
 constexpr int SMALL_UNROLL = 4;  // 8-k groups whose loads are issued before their MFMAs
@@ -400,6 +405,45 @@ __device__ inline floatx4 small_frag(const float* __restrict__ p, int64_t srow, 
     return v;
 }
 
+// Accumulates the 8-k groups g0, g0 + stride, ... (SMALL_UNROLL of them per batch, every load
+// of a batch issued before its MFMAs) of one 32x32 tile into acc. A and B point at the tile's
+// (row 0, k 0); klen is the tile's K extent.
+template <int AM, int BMD, int STRIDE>
+__device__ inline void small_tile_sum(floatx16& acc, const float* A, const float* B,
+                                      const GemmArgs& p, uint32_t g0, uint32_t klen, bool inner,
+                                      bool a_ok, bool b_ok, int r, int h, float alpha_a,
+                                      float alpha_b) {
+    const uint32_t groups = (klen + 7) / 8;
+    for (; g0 < groups; g0 += STRIDE * SMALL_UNROLL) {
+        floatx4 av[SMALL_UNROLL], bv[SMALL_UNROLL];
+        const uint32_t last = g0 + STRIDE * (SMALL_UNROLL - 1);
+        if (inner && 8 * last + 8 <= klen) {
+#pragma unroll
+            for (int u = 0; u < SMALL_UNROLL; ++u) {
+                const uint32_t k0 = 8 * (g0 + STRIDE * u);
+                av[u] = small_frag<AM, true>(A, p.a_sm, p.a_sk, true, k0, klen, r, h);
+                bv[u] = small_frag<BMD, true>(B, p.b_sn, p.b_sk, true, k0, klen, r, h);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < SMALL_UNROLL; ++u) {
+                const uint32_t k0 = 8 * (g0 + STRIDE * u);  // past K: every element predicated to 0
+                av[u] = small_frag<AM, false>(A, p.a_sm, p.a_sk, a_ok, k0, klen, r, h);
+                bv[u] = small_frag<BMD, false>(B, p.b_sn, p.b_sk, b_ok, k0, klen, r, h);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SMALL_UNROLL; ++u) {
+            floatx4 a = av[u], b = bv[u];
+            if (alpha_a != 1.0f) a = a * alpha_a;
+            if (alpha_b != 1.0f) b = b * alpha_b;
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[st], b[st], acc, 0, 0, 0);
+        }
+    }
+}
+
 template <int AM, int BMD, int W = 4>
 __global__ __launch_bounds__(64 * W) void gemm_f32_small(GemmArgs p) {
     constexpr int THREADS = 64 * W;
@@ -408,48 +452,29 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_small(GemmArgs p) {
     const int r = lane & 31, h = lane >> 5;
     uint32_t plane, tm, tn;
     decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
     const uint32_t m0 = tm * SMALL_TILE, n0 = tn * SMALL_TILE;
-    const float* A = p.a + static_cast<int64_t>(plane) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm;
-    const float* B = p.b + static_cast<int64_t>(plane) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn;
+    const uint32_t kb = split * p.k_chunk;
+    const uint32_t klen = min(p.k - kb, p.k_chunk);
+    const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
+                     static_cast<int64_t>(kb) * p.a_sk;
+    const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
+                     static_cast<int64_t>(kb) * p.b_sk;
     const bool inner = p.m - m0 >= SMALL_TILE && p.n - n0 >= SMALL_TILE;
     const bool a_ok = r < static_cast<int>(p.m - m0), b_ok = r < static_cast<int>(p.n - n0);
 
     floatx16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-    const uint32_t groups = (p.k + 7) / 8;
-    // Batches of SMALL_UNROLL of this wave's groups: g = wave + W * (b * SMALL_UNROLL + u).
-    for (uint32_t g0 = wave; g0 < groups; g0 += W * SMALL_UNROLL) {
-        floatx4 av[SMALL_UNROLL], bv[SMALL_UNROLL];
-        const uint32_t last = g0 + W * (SMALL_UNROLL - 1);
-        if (inner && 8 * last + 8 <= p.k) {
-#pragma unroll
-            for (int u = 0; u < SMALL_UNROLL; ++u) {
-                const uint32_t k0 = 8 * (g0 + W * u);
-                av[u] = small_frag<AM, true>(A, p.a_sm, p.a_sk, true, k0, p.k, r, h);
-                bv[u] = small_frag<BMD, true>(B, p.b_sn, p.b_sk, true, k0, p.k, r, h);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < SMALL_UNROLL; ++u) {
-                const uint32_t k0 = 8 * (g0 + W * u);  // past K: every element predicated to 0
-                av[u] = small_frag<AM, false>(A, p.a_sm, p.a_sk, a_ok, k0, p.k, r, h);
-                bv[u] = small_frag<BMD, false>(B, p.b_sn, p.b_sk, b_ok, k0, p.k, r, h);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < SMALL_UNROLL; ++u) {
-            const floatx4 a = av[u] * p.alpha;
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[st], bv[u][st], acc, 0, 0, 0);
-        }
-    }
+    // Wave w takes groups w, w + W, ...
+    small_tile_sum<AM, BMD, W>(acc, A, B, p, wave, klen, inner, a_ok, b_ok, r, h,
+                               p.scale_b ? 1.0f : p.alpha, p.scale_b ? p.alpha : 1.0f);
     // Accumulator register i: row 8*(i/4) + 4*h + i%4, column r.
 #pragma unroll
     for (int i = 0; i < 16; ++i) red[wave][((i >> 2) * 8 + h * 4 + (i & 3)) * SMALL_TILE + r] = acc[i];
     __syncthreads();
-    float* C = p.c + static_cast<int64_t>(plane) * p.c_sb;
+    float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
+    float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
 #pragma unroll
     for (int j = 0; j < SMALL_TILE * SMALL_TILE / THREADS; ++j) {
         const int e = j * THREADS + tid;
@@ -458,9 +483,65 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_small(GemmArgs p) {
             float v = red[0][e];
 #pragma unroll
             for (int w = 1; w < W; ++w) v = v + red[w][e];
-            float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
-            if (p.beta != 0.0f) v = p.beta * *q + v;
-            *q = v;
+            if (p.partial != nullptr) {
+                P[static_cast<int64_t>(row) * p.n + col] = v;
+            } else {
+                float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
+                if (p.beta != 0.0f) v = p.beta * *q + v;
+                *q = v;
+            }
+        }
+    }
+}
+
+// Many small products (batched outputs whose 64x64 or 128x128 tiles would be mostly padding):
+// one 32x32 output tile per wave over its whole K chunk, four tiles per 256-thread workgroup.
+// Operands go straight from memory into MFMA registers, as in gemm_f32_small (no two waves
+// read the same rows, so LDS has nothing to share), and each wave stores its accumulators
+// directly: no LDS, no barrier. Tiles are numbered plane-major (plane = batch * splits +
+// split), row-major within a plane. The sum of one output runs over k in 8-k groups in order.
+constexpr int WAVE_TILES = 4;  // tiles (waves) per workgroup
+
+template <int AM, int BMD>
+__global__ __launch_bounds__(64 * WAVE_TILES) void gemm_f32_wave(GemmArgs p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 31, h = lane >> 5;
+    const uint32_t per_plane = p.tiles_m * p.tiles_n;
+    const uint64_t tile = static_cast<uint64_t>(blockIdx.x) * WAVE_TILES + wave;
+    if (tile >= static_cast<uint64_t>(per_plane) * p.batch * p.splits) return;  // whole wave
+    const uint32_t plane = static_cast<uint32_t>(tile / per_plane);
+    const uint32_t t = static_cast<uint32_t>(tile - static_cast<uint64_t>(plane) * per_plane);
+    const uint32_t tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
+    const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
+    const uint32_t m0 = tm * SMALL_TILE, n0 = tn * SMALL_TILE;
+    const uint32_t kb = split * p.k_chunk;
+    const uint32_t klen = min(p.k - kb, p.k_chunk);
+    const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
+                     static_cast<int64_t>(kb) * p.a_sk;
+    const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
+                     static_cast<int64_t>(kb) * p.b_sk;
+    const bool inner = p.m - m0 >= SMALL_TILE && p.n - n0 >= SMALL_TILE;
+    const bool a_ok = r < static_cast<int>(p.m - m0), b_ok = r < static_cast<int>(p.n - n0);
+    floatx16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    small_tile_sum<AM, BMD, 1>(acc, A, B, p, 0, klen, inner, a_ok, b_ok, r, h,
+                               p.scale_b ? 1.0f : p.alpha, p.scale_b ? p.alpha : 1.0f);
+    // Accumulator register i: row 8*(i/4) + 4*h + i%4, column r.
+    float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
+    float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t row = m0 + (i >> 2) * 8 + h * 4 + (i & 3), col = n0 + r;
+        if (inner || (row < p.m && col < p.n)) {
+            if (p.partial != nullptr) {
+                P[static_cast<int64_t>(row) * p.n + col] = acc[i];
+            } else {
+                float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
+                float v = acc[i];
+                if (p.beta != 0.0f) v = p.beta * *q + v;
+                *q = v;
+            }
         }
     }
 }

@@ -72,15 +72,15 @@ struct Context {
     std::mutex mse_lock;
     void* mse_scratch = nullptr;
     float* mse_host = nullptr;
-    // Split-K partials: one grow-only buffer per context, reused call after call (a
-    // stream-ordered malloc/free per call costs tens of microseconds of host time). split_lock
-    // is held while a call hands the buffer to its two launches. Calls on one stream are
-    // ordered by the stream; a call on another stream first waits for split_event, which
-    // marks the end of the previous user's work.
+    // Split-K partials and the dot path's tickets: one buffer per context, SCRATCH_BYTES long,
+    // allocated with the context (its ticket words zeroed) and never grown, so a split call
+    // never allocates or synchronizes -- also under stream capture. split_lock is held while
+    // a call hands the buffer to its launches. Calls on one stream are ordered by the stream;
+    // an eager call on another stream first waits for split_event, which marks the end of the
+    // previous user's work.
     std::mutex split_lock;
     void* split_scratch = nullptr;
-    uint64_t split_bytes = 0;
-    hipStream_t split_stream = nullptr;  // stream of the last call that used the buffer
+    hipStream_t split_stream = nullptr;  // stream of the last eager call that used the buffer
     hipEvent_t split_event = nullptr;
 };
 void note_launch(Context* ctx, const char* name);
@@ -134,6 +134,13 @@ constexpr uint32_t GEMM_SMALL_K = LG_GEMM_SMALL_K;
 constexpr uint32_t GEMM_BK = 16;       // K-slice depth per LDS stage
 constexpr uint32_t GEMM_THREADS = 256;
 
+// Kernels of the tiled plan.
+enum GemmKernel : uint32_t {
+    KERN_TILE = 0,   // gemm_f32_mfma: 128x128 (or 64x64) tile per 256-thread workgroup
+    KERN_SMALL = 1,  // gemm_f32_small: one 32x32 tile per workgroup, sixteen waves split K
+    KERN_WAVE = 2    // gemm_f32_wave: one 32x32 tile per wave, four tiles per workgroup
+};
+
 struct GemmArgs {
     const float* a;  // element pointer of A's view offset
     const float* b;
@@ -146,8 +153,38 @@ struct GemmArgs {
     uint32_t k_chunk, splits;
     uint32_t tiles_m, tiles_n;
     float alpha, beta;
-    uint32_t tile;  // output tile edge: GEMM_BM (128), GEMM_SMALL_TILE (64) or GEMM_TINY_TILE (32)
+    uint32_t tile;     // output tile edge: GEMM_BM (128), GEMM_SMALL_TILE (64) or GEMM_TINY_TILE (32)
+    uint32_t kernel;   // GemmKernel
+    // 0: alpha scales the A-role operand as it is loaded; 1: the B-role one. The planner swaps
+    // the operands (C^T = B^T.A^T) when C is contiguous along M, and the operand it then
+    // loads as B is the caller's A: every product stays (alpha*a)*b.
+    uint32_t scale_b;
 };
+
+// Dot products (M = N = 1): C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k]. Split along K
+// into `splits` workgroups per product, whose partial sums the last one to finish (a ticket
+// per product) adds in split order.
+struct DotArgs {
+    const float* a;
+    const float* b;
+    float* c;
+    float* partial;     // [batch][splits] when splits > 1
+    uint32_t* tickets;  // [batch] zeroed words when splits > 1; each is zero again afterwards
+    int64_t a_sb, a_sk, b_sb, b_sk, c_sb;
+    uint32_t k, batch, k_chunk, splits;
+    float alpha, beta;
+    uint32_t scale_b;
+};
+constexpr uint32_t DOT_THREADS = 256;
+constexpr uint32_t DOT_MIN_CHUNK = 4096;   // K elements per split, at least
+constexpr uint32_t DOT_TARGET = 2048;      // workgroups the split dot path aims for
+
+// The per-context scratch: TICKET_WORDS ticket words, then split partials. Plans never need
+// more partial bytes than SPLIT_PARTIAL_MAX (the planner caps the split count to fit).
+constexpr uint64_t TICKET_WORDS = 4096;
+constexpr uint64_t TICKET_BYTES = TICKET_WORDS * 4;
+constexpr uint64_t SPLIT_PARTIAL_MAX = 32ull << 20;
+constexpr uint64_t SCRATCH_BYTES = TICKET_BYTES + SPLIT_PARTIAL_MAX;
 
 struct ReduceArgs {
     const float* partial;
@@ -155,6 +192,7 @@ struct ReduceArgs {
     int64_t c_sb, c_sm, c_sn;
     uint32_t m, n, batch, splits;
     float beta;
+    uint32_t slices;  // waves that split the split range of each output: 4 or 16
 };
 
 // Right-aligned mixed radix of up to 4 axes (slot 3 fastest); unused slots have extent 1.
@@ -217,9 +255,12 @@ uint64_t gemm_half_workgroups(uint32_t m, uint32_t n, uint32_t batch);
 
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode);
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args);
+void launch_dot(Context* ctx, hipStream_t s, const DotArgs& args, bool vec);
+// Clears `words` 32-bit words with a kernel (graph-capturable, unlike hipMemsetAsync).
+void launch_clear_words(Context* ctx, hipStream_t s, uint32_t* p, uint64_t words);
 void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args);
 void launch_fill(Context* ctx, hipStream_t s, const FillArgs& args);
-uint64_t gemm_workgroups(uint32_t m, uint32_t n, uint32_t batch, uint32_t splits, uint32_t tile);
+uint64_t gemm_workgroups(const GemmArgs& args);
 
 // ---------------------------------------------------------------------------------------
 // Permutation kernels
@@ -299,6 +340,14 @@ void set_device(const lg_ctx* ctx);
 // f32 kernels; F16 and BF16 the 16-bit ones (f64 sums of exact products, one rounding).
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
                         float beta, const View& c, uint32_t dtype);
+// Plans C = alpha*A.B + beta*C (the gemm form, f32) and enqueues it on `stream` with device
+// scratch from the caller: once validation and planning have passed, and only when the plan
+// needs scratch, `scratch(ctx, s)` is called with the context's device current and returns
+// TICKET_WORDS ticket words that are zero, followed by `partial_cap` bytes for split partials.
+// A plan needing more than partial_cap fails with InvalidArgument before anything is launched.
+void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                const lg_view* b, float beta, const lg_view* c,
+                                uint64_t partial_cap, uint32_t* (*scratch)(lg_ctx*, hipStream_t));
 inline hipStream_t pick_stream(const lg_ctx* ctx, void* stream) {
     return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 }

@@ -21,7 +21,8 @@ CORE_ERRORS = ["Ok", "Shape", "Dtype", "UnsupportedLayout", "UnsupportedDevice",
                "Transport", "Wire", "Schedule"]
 LG_DTYPE_F32, LG_DTYPE_F16, LG_DTYPE_BF16 = 1, 2, 3
 LG_WIRE_HEADER_MAX = 48
-PLAN_KINDS = ["empty", "zero", "scale", "tiled", "split", "general"]
+PLAN_KINDS = ["empty", "zero", "scale", "tiled", "split", "general", "dot"]
+PLAN_KERNELS = ["none", "tile", "small", "wave", "dot"]
 LOAD_MODES = ["k", "mn", "strided"]
 PERMUTE_KINDS = ["empty", "copy", "tile"]
 
@@ -38,7 +39,7 @@ class lg_contract_plan(ctypes.Structure):
     _fields_ = [("kind", u32), ("a_mode", u32), ("b_mode", u32), ("groups", u32),
                 ("batch", u64), ("m", u64), ("n", u64), ("k", u64), ("splits", u64),
                 ("k_chunk", u64), ("workgroups", u64), ("scratch_bytes", u64), ("tile_m", u32),
-                ("tile_n", u32)]
+                ("tile_n", u32), ("kernel", u32), ("swapped", u32)]
 
 
 class lg_permute_plan(ctypes.Structure):

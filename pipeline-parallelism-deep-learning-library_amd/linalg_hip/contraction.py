@@ -84,7 +84,8 @@ def _plan_dict(p: N.lg_contract_plan) -> dict:
             "b_mode": N.LOAD_MODES[p.b_mode], "groups": p.groups, "batch": p.batch, "m": p.m,
             "n": p.n, "k": p.k, "splits": p.splits, "k_chunk": p.k_chunk,
             "workgroups": p.workgroups, "scratch_bytes": p.scratch_bytes,
-            "tile": (p.tile_m, p.tile_n)}
+            "tile": (p.tile_m, p.tile_n), "kernel": N.PLAN_KERNELS[p.kernel],
+            "swapped": bool(p.swapped)}
 
 
 def plan_contract(alpha: float, a, b, beta: float, c) -> dict:

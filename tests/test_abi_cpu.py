@@ -232,6 +232,50 @@ def test_output_tile_choice():
     assert C.plan_gemm(1.0, h([300, 40]), h([40, 300]), 0.0, h([300, 300]))["tile"] == (64, 64)
 
 
+def test_contraction_plans_for_the_reference_benchmark_shapes():
+    """The shapes of tests/contraction_test.rs:1293-1395 (bench_other_paths): no output is padded
+    past half of its tiles, C stored column-major is computed as C^T = B^T.A^T, and dot products
+    run on the VALU."""
+    t = lambda r, c: view(Layout.transposed(r, c))
+    # "transposed 2048": A, B and C all column-major.
+    p = C.plan_contract(1.0, (t(2048, 2048), "mk"), (t(2048, 2048), "kn"), 0.0,
+                        (t(2048, 2048), "mn"))
+    assert p["swapped"] and (p["a_mode"], p["b_mode"]) == ("k", "mn")
+    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "tile", (128, 128), 256)
+    # "batched 4096 x 32^3": one 32x32 tile per wave, four per workgroup.
+    p = C.plan_contract(1.0, (dense([4096, 32, 32]), "bmk"), (dense([4096, 32, 32]), "bkn"), 0.0,
+                        (dense([4096, 32, 32]), "bmn"))
+    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "wave", (32, 32), 1024)
+    # "dot K=16M": split along K on the VALU, partials added in order by the last workgroup.
+    p = C.plan_contract(1.0, (dense([1, 1 << 24]), "mk"), (dense([1 << 24, 1]), "kn"), 0.0,
+                        (dense([1, 1]), "mn"))
+    assert (p["kind"], p["kernel"], p["a_mode"]) == ("dot", "dot", "k")
+    assert p["splits"] * p["k_chunk"] >= 1 << 24 and p["k_chunk"] % 1024 == 0
+    assert p["workgroups"] == p["splits"] == 2048 and p["scratch_bytes"] == 4 * 2048
+    # "32x32 K=1M" (B column-major): sixteen waves per 32x32 tile, split along K.
+    p = C.plan_contract(1.0, (dense([32, 1 << 20]), "mk"), (t(1 << 20, 32), "kn"), 0.0,
+                        (dense([32, 32]), "mn"))
+    assert (p["kind"], p["kernel"], p["tile"]) == ("split", "small", (32, 32))
+    assert (p["a_mode"], p["b_mode"]) == ("k", "k") and p["workgroups"] == p["splits"] == 512
+    assert p["scratch_bytes"] == 512 * 32 * 32 * 4 <= 32 << 20
+    # "rank-1 4096^2" and "rank-4 ijkl,klmn->ijmn 48^6" (axes merge to a 2304^3 product).
+    p = C.plan_contract(1.0, (dense([4096, 1]), "mk"), (dense([1, 4096]), "kn"), 0.0,
+                        (dense([4096, 4096]), "mn"))
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (128, 128), 1024)
+    p = C.plan_contract(1.0, (dense([48] * 4), "ijkl"), (dense([48] * 4), "klmn"), 0.0,
+                        (dense([48] * 4), "ijmn"))
+    assert (p["kind"], p["groups"], p["m"], p["n"], p["k"]) == ("tiled", 1, 2304, 2304, 2304)
+    # Batched dot products (no split once the batch fills the chip) and a skinny output.
+    p = C.plan_contract(1.0, (dense([4096, 1, 512]), "bmk"), (dense([4096, 512, 1]), "bkn"), 0.0,
+                        (dense([4096, 1, 1]), "bmn"))
+    assert (p["kind"], p["splits"], p["workgroups"]) == ("dot", 1, 4096)
+    p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 16]), 0.0, dense([4096, 16]))
+    assert p["tile"] == (32, 32) and p["kernel"] == "small" and p["kind"] == "split"
+    # The split count is capped so the partials fit the context's 32 MiB scratch.
+    p = C.plan_gemm(1.0, dense([1536, 65536]), dense([65536, 1536]), 0.0, dense([1536, 1536]))
+    assert p["kind"] == "split" and p["scratch_bytes"] <= 32 << 20
+
+
 def test_contraction_plans_for_the_baseline_configs():
     p = C.plan_gemm(1.0, dense([512, 512]), dense([512, 512]), 0.0, dense([512, 512]))
     assert p["kind"] in ("tiled", "split") and p["a_mode"] == "k" and p["b_mode"] == "mn"

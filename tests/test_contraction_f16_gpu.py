@@ -240,3 +240,42 @@ def test_repeated_f16_gemm_is_bitwise_stable(ctx, pool):
         C.gemm(ctx, 1.0, a.view(), b.view(), 0.0, c.view())
         outs.append(c.read().view(np.uint16).copy())
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+
+
+def test_gemm_nowait_f16_is_ordered_before_a_download(ctx, pool):
+    """gemm_nowait (src/ops/contraction.rs:1116-1130) enqueues on the context stream and
+    returns; a download, ordered after it on that stream, sees the exact result. A second
+    gemm_nowait reading the first one's output, with no wait between them, sees it too."""
+    g = rng(41)
+    m, n, k = 96, 80, 64
+    a = Half(pool, Layout.dense([m, k]), grid_halves(g, m * k))
+    b = Half(pool, Layout.dense([k, n]), grid_halves(g, k * n))
+    c = Half(pool, Layout.dense([m, n]), np.full(m * n, np.nan, np.float16))
+    sq = Half(pool, Layout.dense([n, n]), grid_halves(g, n * n))
+    d = Half(pool, Layout.dense([m, n]), np.full(m * n, np.nan, np.float16))
+    C.gemm_nowait(ctx, 0.5, a.view(), b.view(), 0.0, c.view())
+    C.gemm_nowait(ctx, 1.0, c.view(), sq.view(), 0.0, d.view())
+    got_c, got_d = c.read(), d.read()
+    want_c = oracle.contract_exact_f16(0.5, a.logical(), b.logical(), 0.0, np.zeros((m, n)))
+    assert f16_bits_equal(got_c[: m * n].reshape(m, n), want_c)
+    c_exact = got_c[: m * n].reshape(m, n)
+    want_d = oracle.contract_exact_f16(1.0, c_exact, sq.logical(), 0.0, np.zeros((m, n)))
+    assert f16_bits_equal(got_d[: m * n].reshape(m, n), want_d)
+
+
+def test_square_2048_exact_inputs_round_once_bit_for_bit(ctx, pool):
+    """The reference's f16 benchmark shape (tests/contraction_test.rs:1345-1352) at full size on
+    halves of the 2^-10 grid: every partial sum is a multiple of 2^-20 below 2^13 in magnitude,
+    so an f64 matmul in any order is exact, and each output must be that value rounded once to
+    f16 (round to nearest even)."""
+    n = 2048
+    g = rng(2048)
+    x = grid_halves(g, n * n)
+    y = grid_halves(g, n * n)
+    a = Half(pool, Layout.dense([n, n]), x)
+    b = Half(pool, Layout.dense([n, n]), y)
+    c = Half(pool, Layout.dense([n, n]), np.full(n * n, np.nan, np.float16))
+    C.gemm(ctx, 1.0, a.view(), b.view(), 0.0, c.view())
+    exact = x.astype(np.float64).reshape(n, n) @ y.astype(np.float64).reshape(n, n)
+    want = exact.astype(np.float16).view(np.uint16)
+    assert f16_bits_equal(c.read()[: n * n].reshape(n, n), want)

@@ -7,8 +7,9 @@ and, for 2-D gemm cases, against the crates/cpu restatement with the north-star 
   max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|.
 Every buffer element outside C's view must keep its bits; with beta = 0, C starts as NaN.
 The case list restates tests/contraction_test.rs (the 20 typed cases for f32 and the 96-case
-random sweep); the benchmark configurations run at full size with row samples checked against
-the oracle and size-independent properties (determinism, linearity) on the whole output.
+random sweep); the benchmark configurations run at full size with every output element checked
+against the oracle (config 5's two gradient products: one whole row in every 128-row tile band)
+and size-independent properties (determinism, linearity) on the whole output.
 """
 from __future__ import annotations
 
@@ -557,10 +558,19 @@ def _dummy_view(pool, layout):
 # benchmark configurations at full size
 # --------------------------------------------------------------------------------------
 def _rows_check(name, got_rows, want_rows, k, amax, bmax):
+    """The north-star bound on every element given: max|err| <= 1e-5*sqrt(K)*max|a|*max|b|."""
     tol = 1e-5 * np.sqrt(k) * amax * bmax
-    err = float(np.max(np.abs(got_rows.astype(np.float64) - want_rows.astype(np.float64))))
-    assert err <= tol, f"{name}: max|err| {err:e} > {tol:e}"
-    return err
+    err = np.abs(got_rows.astype(np.float64) - want_rows.astype(np.float64))
+    worst = int(np.argmax(err))
+    assert err[worst] <= tol and np.all(np.isfinite(got_rows)), (
+        f"{name}: max|err| {err[worst]:e} > {tol:e} at element {worst}")
+    return float(err[worst])
+
+
+def _one_row_per_tile(g, rows, tile=128):
+    """One random row inside every `tile`-row band: every M-tile row of the grid is checked."""
+    return np.array([t + int(g.integers(0, min(tile, rows - t))) for t in range(0, rows, tile)],
+                    dtype=np.uint64)
 
 
 def test_config1_gemm_512_full_oracle(ctx, pool):
@@ -594,15 +604,13 @@ def test_config3_batched_with_permuted_b(ctx, pool):
     assert plan["kind"] == "tiled" and plan["b_mode"] == "k"
     C.contract(ctx, 1.0, (A.view(), "bik"), (bview, "bkj"), 0.0, (Cc.view(), "bij"))
     got = Cc.read()[: bsz * m * m]
-    rows = rng(55).choice(m, 16, replace=False)
-    for bi in [0, 13, 31]:
+    # Every output of every batch against crates/cpu's layout (RM, Transposed, RM):
+    # B[k][j] = Bstore[j][k], strides [1, K].
+    for bi in range(bsz):
         ref = np.zeros(m * m, np.float32)
-        # crates/cpu layout (RM, Transposed, RM): B[k][j] = Bstore[j][k], strides [1, K].
         oracle.gemm_fast(m, m, m, 1.0, 0.0, a, bi * m * m, (m, 1), bstore, bi * m * m, (1, m),
-                         ref, 0, (m, 1), rows=rows)
-        for r in rows:
-            _rows_check(f"config 3 batch {bi} row {r}", got[bi * m * m + r * m: bi * m * m + (r + 1) * m],
-                        ref[r * m:(r + 1) * m], m, 1.0, 1.0)
+                         ref, 0, (m, 1))
+        _rows_check(f"config 3 batch {bi}", got[bi * m * m:(bi + 1) * m * m], ref, m, 1.0, 1.0)
 
 
 def test_config4_split_k_full_oracle_and_deterministic(ctx, pool):
@@ -643,24 +651,28 @@ def test_config5_linear_layer_step(ctx, pool):
     C.gemm(ctx, 1.0, X.view(), W.view(), 0.0, Y.view())
     C.gemm(ctx, 1.0, DY.view(), Wt, 0.0, DX.view())
     C.gemm(ctx, 1.0, Xt, DY.view(), 1.0, DW.view())   # dW starts at zero, beta = 1 accumulates
-    y, dx, dw = Y.read(), DX.read(), DW.read()
-    rows = rng(99).choice(M, 8, replace=False)
+    y, dx, dw = Y.read()[: M * N], DX.read()[: M * K], DW.read()[: K * N]
     ax, aw, ady = (float(np.abs(t).max()) for t in (x, w, dy))
+    # Y = X.W: every element.
     ref = np.zeros(M * N, np.float32)
-    oracle.gemm_fast(M, N, K, 1.0, 0.0, x, 0, (K, 1), w, 0, (N, 1), ref, 0, (N, 1), rows=rows)
-    for r in rows:
-        _rows_check(f"Y row {r}", y[r * N:(r + 1) * N], ref[r * N:(r + 1) * N], K, ax, aw)
+    oracle.gemm_fast(M, N, K, 1.0, 0.0, x, 0, (K, 1), w, 0, (N, 1), ref, 0, (N, 1))
+    _rows_check("Y", y, ref, K, ax, aw)
+    # dX and dW: one whole row inside every 128-row tile band (all 32 M-tiles, every column).
+    rows = _one_row_per_tile(rng(99), M)
     ref = np.zeros(M * K, np.float32)
     oracle.gemm_fast(M, K, N, 1.0, 0.0, dy, 0, (N, 1), w, 0, (1, N), ref, 0, (K, 1), rows=rows)
     for r in rows:
+        r = int(r)
         _rows_check(f"dX row {r}", dx[r * K:(r + 1) * K], ref[r * K:(r + 1) * K], N, ady, aw)
+    rows = _one_row_per_tile(rng(98), K)
     ref = np.zeros(K * N, np.float32)
     oracle.gemm_fast(K, N, M, 1.0, 1.0, x, 0, (1, K), dy, 0, (N, 1), ref, 0, (N, 1), rows=rows)
     for r in rows:
+        r = int(r)
         _rows_check(f"dW row {r}", dw[r * N:(r + 1) * N], ref[r * N:(r + 1) * N], M, ax, ady)
 
 
-def test_gemm_4096_cubed_rows_and_linearity(ctx, pool):
+def test_gemm_4096_cubed_full_oracle_and_linearity(ctx, pool):
     n = 4096
     a = rng(12).uniform(-1, 1, n * n).astype(np.float32)
     b = rng(13).uniform(-1, 1, n * n).astype(np.float32)
@@ -671,8 +683,35 @@ def test_gemm_4096_cubed_rows_and_linearity(ctx, pool):
     C.gemm(ctx, 2.0, A.view(), B.view(), 0.0, C2.view())
     c1, c2 = C1.read()[: n * n], C2.read()[: n * n]
     assert np.array_equal((c1 * np.float32(2)).view(np.uint32), c2.view(np.uint32))
-    rows = rng(77).choice(n, 8, replace=False)
+    # Every output element against the crates/cpu restatement.
     ref = np.zeros(n * n, np.float32)
-    oracle.gemm_fast(n, n, n, 1.0, 0.0, a, 0, (n, 1), b, 0, (n, 1), ref, 0, (n, 1), rows=rows)
-    for r in rows:
-        _rows_check(f"4096^3 row {r}", c1[r * n:(r + 1) * n], ref[r * n:(r + 1) * n], n, 1.0, 1.0)
+    oracle.gemm_fast(n, n, n, 1.0, 0.0, a, 0, (n, 1), b, 0, (n, 1), ref, 0, (n, 1))
+    _rows_check("4096^3", c1, ref, n, 1.0, 1.0)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 100), (256, 256, 8192)])
+def test_gemm_nowait_is_ordered_before_a_download(ctx, pool, m, n, k):
+    """gemm_nowait (src/ops/contraction.rs:1116-1130) enqueues on the context stream and returns
+    before the device finishes; a download (ordered after it on that stream) sees the result,
+    bit for bit what the synchronous gemm stores. A second gemm_nowait that reads the first one's
+    output, with no wait between them, sees the finished values. (256x256x8192 is split-K.)"""
+    g = rng(m + n + k)
+    a = g.uniform(-1, 1, m * k).astype(np.float32)
+    b = g.uniform(-1, 1, k * n).astype(np.float32)
+    sq = g.uniform(-1, 1, n * n).astype(np.float32)
+    A = Tensor(pool, Layout.dense([m, k]), a)
+    B = Tensor(pool, Layout.dense([k, n]), b)
+    SQ = Tensor(pool, Layout.dense([n, n]), sq)
+    nan = np.full(m * n, np.nan, np.float32)
+    C1, C2, D = (Tensor(pool, Layout.dense([m, n]), nan) for _ in range(3))
+    C.gemm(ctx, 1.0, A.view(), B.view(), 0.0, C1.view())
+    assert C.gemm_nowait(ctx, 1.0, A.view(), B.view(), 0.0, C2.view()) is ctx.queue
+    C.gemm_nowait(ctx, 1.0, C2.view(), SQ.view(), 0.0, D.view())
+    c1, c2, d = C1.read()[: m * n], C2.read()[: m * n], D.read()[: m * n]
+    assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
+    ref = np.zeros(m * n, np.float32)
+    oracle.gemm_fast(m, n, k, 1.0, 0.0, a, 0, (k, 1), b, 0, (n, 1), ref, 0, (n, 1))
+    _rows_check("gemm_nowait C", c2, ref, k, 1.0, 1.0)
+    ref2 = np.zeros(m * n, np.float32)
+    oracle.gemm_fast(m, n, n, 1.0, 0.0, c2, 0, (n, 1), sq, 0, (n, 1), ref2, 0, (n, 1))
+    _rows_check("gemm_nowait D", d, ref2, n, float(np.abs(c2).max()), 1.0)

@@ -3,7 +3,7 @@
 Restates the cases of tests/permutation_test.rs over the C ABI: destinations start as
 SENTINEL words and every word outside the destination view must survive; sources mix random
 words and SPECIALS (NaN payloads, -0, infinities, subnormals); all element types (f32, u32,
-complex f32). The benchmark configurations run at full size and are compared word for word
+i32, complex f32). The benchmark configurations run at full size and are compared word for word
 with numpy.transpose of the raw bits.
 """
 from __future__ import annotations
@@ -20,7 +20,7 @@ from linalg_hip import permutation as P
 
 pytestmark = pytest.mark.gpu
 
-TYPES = ["f32", "u32", "c64"]
+TYPES = ["f32", "u32", "i32", "c64"]
 
 
 def check_all_perms(ctx, pool, dtype, base, seed):
