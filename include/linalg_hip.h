@@ -185,6 +185,17 @@ lg_status lg_gemm_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view*
 lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b,
                              float beta, const lg_view* c);
 
+/* No counterpart in the reference: lg_encode_gemm_f32 for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * Same arguments, validation, plans and results as lg_encode_gemm_f32. It allocates nothing:
+ * split-K partials and dot-product tickets live in a static device array that each GPU holds
+ * until the process ends, 32 MiB of partials plus 16 KiB of ticket words (no plan needs more;
+ * a product that did would fail with LG_INVALID_ARGUMENT before launching anything). Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU race on it and must
+ * be ordered by the caller (one stream, or events). */
+lg_status lg_encode_gemm_f32_noalloc(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
+                                     const lg_view* b, float beta, const lg_view* c);
+
 /* The same five entry points for half operands: contract / gemm / gemm_nowait instantiated at
  * `T = half::f16` (src/ops/contraction.rs:22-32,147-162,1036-1130). Views are in f16
  * elements (2 bytes, 2-byte aligned base); alpha and beta stay f32. Validation, label and

@@ -35,6 +35,7 @@ SOURCES = [
     "permutation.cpp",
     "wire.cpp",
     "contraction_kernels.hip",
+    "contraction_noalloc.hip",
     "contraction_f16_kernels.hip",
     "permutation_kernels.hip",
     "training_kernels.hip",

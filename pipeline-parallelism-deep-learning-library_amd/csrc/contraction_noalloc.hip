@@ -1,0 +1,60 @@
+// lg_encode_gemm_f32_noalloc: lg_encode_gemm_f32 for callers that may not allocate device
+// memory (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+//
+// Its split-K partials and dot-product tickets live in `scratch`, a file-scope device array of
+// SCRATCH_BYTES (16 KiB of ticket words + 32 MiB of partials, the most any plan uses: the
+// planner caps split counts to fit), which each GPU holds from the library's first use on it
+// until the process ends. In host code the array's name is only a stand-in: its device address
+// on each GPU is looked up once per device with hipGetSymbolAddress, on the entry point's first
+// call there, and only that address is handed to kernels. The same first call clears the
+// ticket words with a kernel on the caller's stream (a kernel, so the call may be captured),
+// and every call leaves them at zero again. Every call on one GPU shares that GPU's array, so
+// calls that overlap on one GPU (several streams, several contexts, or graph replays running
+// at once) race on it: the caller orders them. Nothing here allocates: no hipMalloc, no
+// hipFree, no allocating library routine.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "lg_internal.h"
+
+namespace lg {
+namespace {
+
+static_assert(SCRATCH_BYTES % 256 == 0, "scratch is whole 256-byte granules");
+static __device__ __align__(256) uint32_t scratch[SCRATCH_BYTES / sizeof(uint32_t)];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex table_lock;
+void* table[MAX_DEVICES] = {};  // device address of `scratch` on each device, once looked up
+
+// The device address of `scratch` on the context's device (current when called), looked up and
+// its tickets cleared on `s` the first time.
+uint32_t* scratch_on(lg_ctx* ctx, hipStream_t s) {
+    const int device = ctx->device;
+    if (device < 0 || device >= MAX_DEVICES) fail_invalid("device index beyond the scratch table");
+    std::lock_guard<std::mutex> hold(table_lock);
+    if (table[device] == nullptr) {
+        void* ptr = nullptr;
+        check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (ptr == nullptr) fail_kernel("hipGetSymbolAddress(scratch) returned no address");
+        launch_clear_words(ctx, s, static_cast<uint32_t*>(ptr), TICKET_WORDS);
+        table[device] = ptr;
+    }
+    return static_cast<uint32_t*>(table[device]);
+}
+
+}  // namespace
+}  // namespace lg
+
+using namespace lg;
+
+extern "C" lg_status lg_encode_gemm_f32_noalloc(lg_ctx* ctx, void* stream, float alpha,
+                                                const lg_view* a, const lg_view* b, float beta,
+                                                const lg_view* c) {
+    return guarded([&] {
+        if (ctx == nullptr) fail_invalid("null context");
+        enqueue_gemm_fixed_scratch(ctx, stream, alpha, a, b, beta, c, SCRATCH_BYTES - TICKET_BYTES,
+                                   scratch_on);
+    });
+}

@@ -86,6 +86,7 @@ SIGNATURES = {
     "lg_encode_gemm_f32": (i32, [vp, vp, F, VP, VP, F, VP]),
     "lg_gemm_f32": (i32, [vp, F, VP, VP, F, VP]),
     "lg_gemm_nowait_f32": (i32, [vp, F, VP, VP, F, VP]),
+    "lg_encode_gemm_f32_noalloc": (i32, [vp, vp, F, VP, VP, F, VP]),
     "lg_backend_gemm": (i32, [vp, vp, TP, TP, TP, F, F]),
     "lg_backend_gelu": (i32, [vp, vp, TP, TP]),
     "lg_backend_gelu_backward": (i32, [vp, vp, TP, TP, TP]),
