@@ -574,10 +574,13 @@ def main() -> int:
                          "of sustained MFMA load to reach its steady clock (5 launches of the "
                          "4096^3 GEMM measure ~7%% below steady state)")
     ap.add_argument("--only", default=None,
-                    help="run one workload: gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, "
+                    help="run only these workloads (comma-separated): gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, "
                          "train, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, o_rank4, "
                          "o_f16_2048")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--prewarm", type=float, default=0.0,
+                    help="seconds of 4096^3 GEMMs to run before any timing, so workloads timed "
+                         "alone start at the steady shader clock")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
@@ -610,8 +613,20 @@ def main() -> int:
     only = args.only
     results = {}
 
+    wanted = None if only is None else set(only.split(","))
+    if args.prewarm > 0:
+        pool_warm = [L.alloc_shared(ctx, "f32", 4096 * 4096) for _ in range(3)]
+        vs = [L.TensorView.row_major(b, 0, [4096, 4096]) for b in pool_warm]
+        t_end = time.perf_counter() + args.prewarm
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                C.encode_gemm(ctx, ctx.queue, 1.0, vs[0], vs[1], 0.0, vs[2])
+            ctx.sync()
+        for b in pool_warm:
+            b.free()
+
     def run(name, fn):
-        if only is None or only == name:
+        if wanted is None or name in wanted:
             print(f"[bench] {name} ...", file=sys.stderr, flush=True)
             results[name] = fn()
             pool.free()

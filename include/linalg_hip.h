@@ -188,11 +188,11 @@ lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const l
 /* No counterpart in the reference: lg_encode_gemm_f32 for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
  * Same arguments, validation, plans and results as lg_encode_gemm_f32. It allocates nothing:
- * split-K partials and dot-product tickets live in a static device array that each GPU holds
- * until the process ends, 32 MiB of partials plus 16 KiB of ticket words (no plan needs more;
- * a product that did would fail with LG_INVALID_ARGUMENT before launching anything). Every
- * call on one GPU shares that GPU's array, so calls that overlap on one GPU race on it and must
- * be ordered by the caller (one stream, or events). */
+ * split-K and split-dot partials live in a static device array of 32 MiB that each GPU holds
+ * until the process ends (no plan needs more; a product that did would fail with
+ * LG_INVALID_ARGUMENT before launching anything). Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU race on it and must be ordered by the caller (one
+ * stream, or events). */
 lg_status lg_encode_gemm_f32_noalloc(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
                                      const lg_view* b, float beta, const lg_view* c);
 
@@ -390,7 +390,9 @@ typedef enum lg_plan_kernel {
     LG_KERNEL_TILE = 1,  /* 128x128 (or 64x64) output tile per 256-thread workgroup */
     LG_KERNEL_SMALL = 2, /* one 32x32 tile per workgroup, sixteen waves splitting its K */
     LG_KERNEL_WAVE = 3,  /* one 32x32 tile per wave (batches of small products) */
-    LG_KERNEL_DOT = 4    /* one dot product (chunk) per workgroup */
+    LG_KERNEL_DOT = 4,   /* one dot product (chunk) per workgroup */
+    LG_KERNEL_OUTER = 5, /* K <= 8: four outputs per thread on the VALU, summed in k order */
+    LG_KERNEL_DIRECT = 6 /* 128x128 or 128x256 tile, operand slices loaded straight into LDS */
 } lg_plan_kernel;
 
 /* Operand load modes of the tiled kernel. */
@@ -410,11 +412,12 @@ typedef struct lg_contract_plan {
     uint64_t k_chunk;     /* K elements per split */
     uint64_t workgroups;  /* workgroups of the main launch */
     uint64_t scratch_bytes; /* device scratch of the split-K partials */
-    uint32_t tile_m;      /* output tile of one workgroup or wave (tiled/split): 128x128; */
-    uint32_t tile_n;      /* 64x64 when 128x128 tiles would leave most compute units idle or
-                             be mostly padding; 32x32 for small outputs (sixteen waves per tile
-                             splitting K) and batches of small products (one tile per wave);
-                             1x1 for dot products; f16: 64x64 */
+    uint32_t tile_m;      /* output tile of one workgroup or wave (tiled/split): 128x256 for */
+    uint32_t tile_n;      /* grids of at least 512 such tiles, else 128x128; 64x64 when 128x128
+                             tiles would leave most compute units idle or be mostly padding;
+                             32x32 for small outputs (sixteen waves per tile splitting K) and
+                             batches of small products (one tile per wave); 1x1 for dot
+                             products, 1x4 for K <= 8; f16: 64x64 */
     uint32_t kernel;      /* lg_plan_kernel */
     uint32_t swapped;     /* 1 when C is contiguous along M and is computed as C^T = B^T.A^T */
 } lg_contract_plan;

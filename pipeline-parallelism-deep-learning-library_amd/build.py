@@ -66,6 +66,18 @@ def _compile(src: str, obj: Path = OBJ, sanitize: bool = False) -> Path:
     return out
 
 
+def check_stubs(lib: Path) -> None:
+    """Fails when a kernel's host-side launch stub is left undefined: clang emits no stub for a
+    kernel template whose host-side instantiation it drops, and the library would then load
+    nowhere."""
+    res = subprocess.run(["nm", "-D", "--undefined-only", str(lib)], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"nm failed on {lib}: {res.stderr}")
+    missing = [ln.split()[-1] for ln in res.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        raise RuntimeError(f"{lib}: kernels without a launch stub: {missing}")
+
+
 def build(verbose: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
@@ -76,6 +88,7 @@ def build(verbose: bool = False) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    check_stubs(tmp)
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

@@ -190,11 +190,10 @@ lg_status lg_ctx_create(int32_t device, lg_ctx** out) {
         ctx->device = device;
         for (auto& n : ctx->names) n.store(nullptr);
         check_hip(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
-        // The split-K / dot scratch, made once here so no enqueue ever allocates (stream capture
-        // included); its ticket words start at zero and every call leaves them at zero.
+        // The split partials' scratch, made once here so no enqueue ever allocates (stream
+        // capture included).
         void* scratch = nullptr;
         hipError_t err = hipMalloc(&scratch, SCRATCH_BYTES);
-        if (err == hipSuccess) err = hipMemset(scratch, 0, TICKET_BYTES);
         if (err == hipSuccess) err = hipEventCreateWithFlags(&ctx->split_event, hipEventDisableTiming);
         if (err != hipSuccess) {
             if (scratch != nullptr) (void)hipFree(scratch);

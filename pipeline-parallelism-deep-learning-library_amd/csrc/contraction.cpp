@@ -539,11 +539,11 @@ void small_split_shape(uint64_t tiles, uint32_t k, uint64_t split_bytes, uint32_
 }
 
 // The dot path's split: DOT_TARGET workgroups in all, each chunk at least DOT_MIN_CHUNK and a
-// multiple of 1024 (four elements for each of 256 threads), at most TICKET_WORDS products.
+// multiple of 1024 (four elements for each of 256 threads).
 void dot_split_shape(uint32_t batch, uint32_t k, uint32_t* splits, uint32_t* chunk) {
     *splits = 1;
     *chunk = k;
-    if (batch >= DOT_TARGET / 2 || batch > TICKET_WORDS || k < 2 * DOT_MIN_CHUNK) return;
+    if (batch >= DOT_TARGET / 2 || k < 2 * DOT_MIN_CHUNK) return;
     const uint64_t want = (DOT_TARGET + batch - 1) / batch;
     const uint64_t rough = std::max<uint64_t>(
         1, std::min<uint64_t>({want, k / DOT_MIN_CHUNK, SPLIT_PARTIAL_MAX / (4ull * batch)}));
@@ -553,6 +553,9 @@ void dot_split_shape(uint32_t batch, uint32_t k, uint32_t* splits, uint32_t* chu
     *chunk = static_cast<uint32_t>(c);
     *splits = static_cast<uint32_t>((k + c - 1) / c);
 }
+
+// Compute units of one MI355X, for the tile-size choice only.
+constexpr uint64_t GEMM_CUS = 256;
 
 // Waves a many-tile 32x32 product needs before it takes one tile per wave (gemm_f32_wave)
 // rather than sixteen waves per tile (gemm_f32_small).
@@ -716,6 +719,29 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     t.alpha = alpha;
     t.beta = beta;
     t.scale_b = swap ? 1 : 0;
+    if (k <= OUTER_MAX_K) {
+        // Low-rank updates (rank-1 and the like): memory-bound on C, on the VALU in the
+        // reference's own order, four outputs per thread.
+        auto al = [](uint64_t x) { return x % 4 == 0; };
+        t.kernel = KERN_OUTER;
+        t.tile = 1;
+        t.tile_n = 4;
+        t.splits = 1;
+        t.k_chunk = k;
+        t.tiles_m = mm;
+        t.tiles_n = (nn + 3) / 4;
+        t.vec_c = c_sn == 1 && al(nn) && al(c_sm) && al(ab.c) && (c.base + c.offset * 4) % 16 == 0;
+        t.vec_b = rb.srow == 1 && al(nn) && al(rb.sk) && al(rb.sb) &&
+                  (rb.base + rb.offset * 4) % 16 == 0;
+        info.kind = LG_PLAN_TILED;
+        info.kernel = LG_KERNEL_OUTER;
+        info.tile_m = 1;
+        info.tile_n = 4;
+        info.a_mode = LG_LOAD_STRIDED;
+        info.b_mode = t.vec_b ? LG_LOAD_MN_CONTIG : LG_LOAD_STRIDED;
+        info.workgroups = gemm_workgroups(t);
+        return p;
+    }
     // Tile choice. 128x128 tiles load half the operand bytes per product of 64x64 ones, so they
     // are kept whenever at least half of their area is output and their grid, split along K as
     // far as split_shape would go, reaches GEMM_SMALL_BELOW workgroups; otherwise 64x64 tiles
@@ -732,7 +758,16 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
         t.tile = GEMM_TINY_TILE;  // one launch, no split-K partials
         t.kernel = KERN_SMALL;
     } else if (2 * useful >= big * GEMM_BM * GEMM_BN) {
-        t.tile = big * k_ways < GEMM_SMALL_BELOW ? GEMM_SMALL_TILE : GEMM_BM;
+        // A compute unit's time follows the tiles it holds (four 128x128 workgroups share one
+        // at a time), and a 64x64 tile is a quarter of the work at ~0.85 of the efficiency, so
+        // 64x64 tiles also win when the 128x128 grid spreads unevenly over the chip's
+        // GEMM_CUS compute units (2304^3: 324 tiles, 312 -> 272 us) but not when it spreads
+        // evenly (2048^3: 256 tiles, 172 vs 177 us). Grids under GEMM_CUS tiles split along K
+        // instead. The constant is the part's; plans depend on the shape alone.
+        const uint64_t rounds_big = (big + GEMM_CUS - 1) / GEMM_CUS;
+        const uint64_t rounds_mid = (mid + GEMM_CUS - 1) / GEMM_CUS;
+        const bool uneven = big >= GEMM_CUS && 20 * rounds_mid < 68 * rounds_big;
+        t.tile = big * k_ways < GEMM_SMALL_BELOW || uneven ? GEMM_SMALL_TILE : GEMM_BM;
         t.kernel = KERN_TILE;
     } else if (2 * useful >= mid * GEMM_SMALL_TILE * GEMM_SMALL_TILE) {
         t.tile = GEMM_SMALL_TILE;
@@ -741,19 +776,34 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
         t.tile = GEMM_TINY_TILE;
         t.kernel = tiny >= WAVE_MIN_TILES ? KERN_WAVE : KERN_SMALL;
     }
-    t.tiles_m = (mm + t.tile - 1) / t.tile;
-    t.tiles_n = (nn + t.tile - 1) / t.tile;
-    info.tile_m = info.tile_n = t.tile;
-    info.kernel = t.kernel == KERN_TILE ? LG_KERNEL_TILE
-                  : t.kernel == KERN_SMALL ? LG_KERNEL_SMALL : LG_KERNEL_WAVE;
     const int a_mode = load_mode(ra.base, ra.offset, ra.sb, ra.srow, ra.sk);
     const int b_mode = load_mode(rb.base, rb.offset, rb.sb, rb.srow, rb.sk);
     info.a_mode = static_cast<uint32_t>(a_mode);
     info.b_mode = static_cast<uint32_t>(b_mode);
+    t.tile_n = t.tile;
+    if (t.kernel == KERN_TILE && t.tile == GEMM_BM && a_mode != LOAD_S && b_mode != LOAD_S) {
+        // Both operands have a 16-byte aligned unit-stride axis: slices go straight into LDS.
+        // 128x256 tiles (eight waves, two workgroups per compute unit) when at least
+        // 2 * GEMM_CUS of them fill the chip in whole rounds (4096^3: 131 -> 137 TFLOP/s,
+        // config 5 131 -> 138); otherwise 128x128 tiles, three workgroups per compute unit,
+        // also for split-K.
+        t.kernel = KERN_DIRECT;
+        const uint64_t wide = static_cast<uint64_t>((mm + GEMM_BM - 1) / GEMM_BM) *
+                              ((nn + GEMM_WIDE_N - 1) / GEMM_WIDE_N) * batch;
+        if (wide >= 2 * GEMM_CUS) t.tile_n = GEMM_WIDE_N;
+    }
+    t.tiles_m = (mm + t.tile - 1) / t.tile;
+    t.tiles_n = (nn + t.tile_n - 1) / t.tile_n;
+    info.tile_m = t.tile;
+    info.tile_n = t.tile_n;
+    info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
+                  : t.kernel == KERN_DIRECT ? LG_KERNEL_DIRECT
+                  : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
+                                            : LG_KERNEL_WAVE;
     const uint64_t tiles = static_cast<uint64_t>(t.tiles_m) * t.tiles_n * batch;
     const uint64_t split_bytes = static_cast<uint64_t>(batch) * mm * nn * sizeof(float);
     uint32_t splits = 1, chunk = k;
-    if (t.kernel == KERN_TILE) {
+    if (t.kernel == KERN_TILE || t.kernel == KERN_DIRECT) {
         split_shape(tiles, k, split_bytes, &splits, &chunk);
     } else if (t.kernel == KERN_SMALL && !(mid < GEMM_SMALL_BELOW && k <= GEMM_SMALL_K)) {
         small_split_shape(tiles, k, split_bytes, &splits, &chunk);
@@ -814,11 +864,9 @@ Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, 
     return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta, half);
 }
 
-// Device scratch handed to a split or split-dot plan's launches: ticket words (zero between
-// calls) and the partials.
+// Device scratch handed to a split or split-dot plan's launches: the partials.
 struct Scratch {
     float* partial = nullptr;
-    uint32_t* tickets = nullptr;
 };
 
 bool capturing(hipStream_t s) {
@@ -873,7 +921,6 @@ void launch_plan(lg_ctx* ctx, hipStream_t s, Plan& p, const Scratch& sc) {
             return;
         case LG_PLAN_DOT:
             p.dot.partial = sc.partial;
-            p.dot.tickets = sc.tickets;
             launch_dot(ctx, s, p.dot, p.info.a_mode == LG_LOAD_K_CONTIG);
             return;
     }
@@ -903,8 +950,7 @@ void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
         }
     }
     Scratch sc;
-    sc.tickets = static_cast<uint32_t*>(ctx->split_scratch);
-    sc.partial = reinterpret_cast<float*>(static_cast<char*>(ctx->split_scratch) + TICKET_BYTES);
+    sc.partial = static_cast<float*>(ctx->split_scratch);
     launch_plan(ctx, s, p, sc);
     if (!cap) {
         ctx->split_stream = s;
@@ -927,7 +973,7 @@ void run(lg_ctx* ctx, void* stream, Plan plan, bool wait) {
 
 void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
                                 const lg_view* b, float beta, const lg_view* c,
-                                uint64_t partial_cap, uint32_t* (*scratch)(lg_ctx*, hipStream_t)) {
+                                uint64_t partial_cap, float* (*scratch)(lg_ctx*)) {
     View va, vb, vc;
     Plan plan = plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc);
     if (plan.info.scratch_bytes > partial_cap) {
@@ -938,10 +984,7 @@ void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg
     set_device(ctx);
     hipStream_t s = pick_stream(ctx, stream);
     Scratch sc;
-    if (needs_scratch(plan)) {
-        sc.tickets = scratch(ctx, s);
-        sc.partial = reinterpret_cast<float*>(sc.tickets + TICKET_WORDS);
-    }
+    if (needs_scratch(plan)) sc.partial = scratch(ctx);
     launch_plan(ctx, s, plan, sc);
 }
 

@@ -6,12 +6,16 @@
 // Everything is compiled with -ffp-contract=off: products and sums round separately.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
+#include "gemm_dlds.h"
 #include "gemm_kernel.h"
 #include "lg_internal.h"
 
 namespace lg {
 namespace {
 
+using gemm_detail::gemm_f32_dl;
 using gemm_detail::gemm_f32_mfma;
 using gemm_detail::gemm_f32_small;
 using gemm_detail::gemm_f32_wave;
@@ -92,14 +96,13 @@ __global__ __launch_bounds__(RED_LANES * SL) void reduce_f32(ReduceArgs p) {
 // Dot products, C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k] (M = N = 1, memory-bound:
 // 8 bytes per multiply-add, so the VALU rather than a mostly-padded MFMA tile). Workgroup
 // (b, s) takes K chunk s of product b; thread t sums the elements t, t + 256, ... of the chunk
-// (128-bit runs of 4 when VEC) in index order, and the workgroup adds the 256 thread sums in a
-// fixed tree. With one split that is the result; otherwise it is partial[b][s], and the
-// workgroup that draws the last ticket of product b (a device-scope counter; every partial is
-// released before its ticket is drawn) adds the partials: thread t sums splits t, t + 256, ...
-// in order, then the same tree. It then returns the ticket word to zero for the next call on
-// the scratch. The order depends only on K, the chunk and the split count. Nothing waits on
-// another workgroup, so no schedule can hang.
-constexpr int DOT_UNROLL = 4;  // 128-bit runs whose loads are issued before their products
+// (128-bit runs of 4 when VEC, DOT_UNROLL runs' loads issued before their products) in index
+// order, and the workgroup adds the 256 thread sums in a fixed tree. With one split that is
+// the result; otherwise it is partial[b][s], and dot_finish (the next launch on the stream, so
+// every partial is complete and visible) adds product b's partials: thread t sums splits
+// t, t + 256, ... in order, then the same tree. No workgroup waits on another and no device-
+// scope fence runs per workgroup. The order depends only on K, the chunk and the split count.
+constexpr int DOT_UNROLL = 8;
 
 __device__ inline float dot_tree(float* red, float v) {
     red[threadIdx.x] = v;
@@ -116,7 +119,6 @@ template <bool VEC>
 __global__ __launch_bounds__(DOT_THREADS) void dot_f32(DotArgs p) {
     typedef float vec __attribute__((ext_vector_type(4)));
     __shared__ float red[DOT_THREADS];
-    __shared__ bool last;
     const uint32_t bi = blockIdx.x / p.splits, split = blockIdx.x - bi * p.splits;
     const uint32_t kb = split * p.k_chunk;
     const uint32_t klen = min(p.k - kb, p.k_chunk);
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(DOT_THREADS) void dot_f32(DotArgs p) {
     };
     uint32_t i = threadIdx.x;
     if constexpr (VEC) {
-        // klen is a multiple of 4 except in the last chunk, whose tail the scalar loop takes.
+        // klen is a multiple of 4 except in the last chunk, whose tail the scalar step takes.
         const vec* av = reinterpret_cast<const vec*>(a);
         const vec* bv = reinterpret_cast<const vec*>(b);
         const uint32_t nv = klen / 4;
@@ -161,36 +163,83 @@ __global__ __launch_bounds__(DOT_THREADS) void dot_f32(DotArgs p) {
         }
     }
     const float sum = dot_tree(red, acc);
-    float* c = p.c + static_cast<int64_t>(bi) * p.c_sb;
+    if (threadIdx.x != 0) return;
     if (p.splits == 1) {
-        if (threadIdx.x == 0) *c = p.beta != 0.0f ? p.beta * *c + sum : sum;
-        return;
-    }
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(p.partial + blockIdx.x, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();
-        last = __hip_atomic_fetch_add(p.tickets + bi, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
-               p.splits - 1;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    float t = 0.0f;
-    for (uint32_t g = threadIdx.x; g < p.splits; g += DOT_THREADS) {
-        t = t + __hip_atomic_load(p.partial + static_cast<uint64_t>(bi) * p.splits + g, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const float total = dot_tree(red, t);
-    if (threadIdx.x == 0) {
-        *c = p.beta != 0.0f ? p.beta * *c + total : total;
-        __hip_atomic_store(p.tickets + bi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float* c = p.c + static_cast<int64_t>(bi) * p.c_sb;
+        *c = p.beta != 0.0f ? p.beta * *c + sum : sum;
+    } else {
+        p.partial[blockIdx.x] = sum;
     }
 }
 
-__global__ __launch_bounds__(256) void clear_words(uint32_t* p, uint64_t words) {
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
-         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-        p[i] = 0u;
+// Products with K <= OUTER_MAX_K (rank-1 and other low-rank updates): memory-bound on C, so
+// the VALU does them in crates/cpu's own order, acc = beta == 0 ? +0 : beta*C, then
+// acc = acc + (alpha*a)*b for k in order, one rounding per operation: the reference's bits.
+// Thread t owns four consecutive columns of one row (128-bit loads of B and non-temporal
+// 128-bit stores of C when VB / VC); a grid-stride loop of at most OUTER_MAX_GROUPS workgroups
+// covers batch * m * ceil(n / 4) such quads (measured on rank-1 4096^2: 17.1 -> 15.8 us
+// against one quad per thread with ordinary stores).
+constexpr uint32_t OUTER_THREADS = 256;
+constexpr uint32_t OUTER_MAX_GROUPS = 2048;
+
+template <bool VB, bool VC>
+__global__ __launch_bounds__(OUTER_THREADS) void outer_f32(GemmArgs p) {
+    typedef float vec __attribute__((ext_vector_type(4)));
+    const uint32_t nq = (p.n + 3) / 4;
+    const uint64_t total = static_cast<uint64_t>(p.batch) * p.m * nq;
+    const float alpha_a = p.scale_b ? 1.0f : p.alpha, alpha_b = p.scale_b ? p.alpha : 1.0f;
+    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * OUTER_THREADS + threadIdx.x; t < total;
+         t += static_cast<uint64_t>(gridDim.x) * OUTER_THREADS) {
+        const uint64_t row = t / nq;
+        const uint32_t j0 = static_cast<uint32_t>(t - row * nq) * 4;
+        const uint32_t bi = static_cast<uint32_t>(row / p.m), i = static_cast<uint32_t>(row - static_cast<uint64_t>(bi) * p.m);
+        const uint32_t cnt = min(4u, p.n - j0);
+        const float* a = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(i) * p.a_sm;
+        const float* b = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(j0) * p.b_sn;
+        float* c = p.c + static_cast<int64_t>(bi) * p.c_sb + static_cast<int64_t>(i) * p.c_sm +
+                   static_cast<int64_t>(j0) * p.c_sn;
+        vec acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p.beta != 0.0f) {
+            if constexpr (VC) {
+                acc = p.beta * *reinterpret_cast<const vec*>(c);
+            } else {
+                for (uint32_t e = 0; e < cnt; ++e) acc[e] = p.beta * c[static_cast<int64_t>(e) * p.c_sn];
+            }
+        }
+        for (uint32_t k = 0; k < p.k; ++k) {
+            float x = a[static_cast<int64_t>(k) * p.a_sk];
+            vec y;
+            if constexpr (VB) {
+                y = *reinterpret_cast<const vec*>(b + static_cast<int64_t>(k) * p.b_sk);
+            } else {
+#pragma unroll
+                for (uint32_t e = 0; e < 4; ++e) {
+                    y[e] = e < cnt ? b[static_cast<int64_t>(k) * p.b_sk + static_cast<int64_t>(e) * p.b_sn] : 0.0f;
+                }
+            }
+            if (alpha_a != 1.0f) x = alpha_a * x;
+            if (alpha_b != 1.0f) y = alpha_b * y;
+            acc = acc + x * y;
+        }
+        if constexpr (VC) {
+            __builtin_nontemporal_store(acc, reinterpret_cast<vec*>(c));
+        } else {
+            for (uint32_t e = 0; e < cnt; ++e) c[static_cast<int64_t>(e) * p.c_sn] = acc[e];
+        }
+    }
+}
+
+// Second launch of a split dot: workgroup b adds product b's partials in split order.
+__global__ __launch_bounds__(DOT_THREADS) void dot_finish_f32(DotArgs p) {
+    __shared__ float red[DOT_THREADS];
+    const uint32_t bi = blockIdx.x;
+    const float* part = p.partial + static_cast<uint64_t>(bi) * p.splits;
+    float t = 0.0f;
+    for (uint32_t g = threadIdx.x; g < p.splits; g += DOT_THREADS) t = t + part[g];
+    const float total = dot_tree(red, t);
+    if (threadIdx.x == 0) {
+        float* c = p.c + static_cast<int64_t>(bi) * p.c_sb;
+        *c = p.beta != 0.0f ? p.beta * *c + total : total;
     }
 }
 
@@ -260,7 +309,27 @@ void check_launch(const char* what) { check_hip(hipGetLastError(), what); }
 
 template <int AM, int BMD>
 void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
-    if (a.kernel == KERN_WAVE) {
+    if (a.kernel == KERN_OUTER) {
+        if (a.vec_b && a.vec_c) {
+            hipLaunchKernelGGL((outer_f32<true, true>), dim3(groups), dim3(OUTER_THREADS), 0, s, a);
+        } else if (a.vec_c) {
+            hipLaunchKernelGGL((outer_f32<false, true>), dim3(groups), dim3(OUTER_THREADS), 0, s, a);
+        } else if (a.vec_b) {
+            hipLaunchKernelGGL((outer_f32<true, false>), dim3(groups), dim3(OUTER_THREADS), 0, s, a);
+        } else {
+            hipLaunchKernelGGL((outer_f32<false, false>), dim3(groups), dim3(OUTER_THREADS), 0, s, a);
+        }
+    } else if (a.kernel == KERN_DIRECT) {
+        if constexpr (AM != LOAD_S && BMD != LOAD_S) {
+            if (a.tile_n == GEMM_WIDE_N) {
+                hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 3, 16, 4>), dim3(groups), dim3(512), 0, s, a);
+            } else {
+                hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 3, 16, 2>), dim3(groups), dim3(256), 0, s, a);
+            }
+        } else {
+            fail_invalid("direct-load GEMM needs a unit-stride axis in both operands");
+        }
+    } else if (a.kernel == KERN_WAVE) {
         hipLaunchKernelGGL((gemm_f32_wave<AM, BMD>), dim3(groups), dim3(64 * WAVE_TILES), 0, s, a);
     } else if (a.kernel == KERN_SMALL) {
         hipLaunchKernelGGL((gemm_f32_small<AM, BMD, SMALL_WAVES>), dim3(groups), dim3(64 * SMALL_WAVES), 0,
@@ -269,9 +338,7 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 1, 1>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);
     } else {
-        // A read along M (a transposed A) takes the two-ahead pipeline.
-        constexpr bool ahead = AM == LOAD_MN && BMD != LOAD_S;
-        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 2, 2, ahead>), dim3(groups),
+        hipLaunchKernelGGL((gemm_f32_mfma<AM, BMD, GEMM_BK, 2, 2>), dim3(groups),
                            dim3(GEMM_THREADS), 0, s, a);
     }
 }
@@ -279,14 +346,19 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
 }  // namespace
 
 uint64_t gemm_workgroups(const GemmArgs& a) {
+    if (a.kernel == KERN_OUTER) {
+        const uint64_t quads = static_cast<uint64_t>(a.batch) * a.m * ((a.n + 3) / 4);
+        return std::max<uint64_t>(1, std::min<uint64_t>((quads + OUTER_THREADS - 1) / OUTER_THREADS,
+                                                         OUTER_MAX_GROUPS));
+    }
     const uint64_t tiles = static_cast<uint64_t>((a.m + a.tile - 1) / a.tile) *
-                           ((a.n + a.tile - 1) / a.tile) * a.batch * a.splits;
+                           ((a.n + a.tile_n - 1) / a.tile_n) * a.batch * a.splits;
     return a.kernel == KERN_WAVE ? (tiles + WAVE_TILES - 1) / WAVE_TILES : tiles;
 }
 
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode) {
     const uint32_t groups = static_cast<uint32_t>(gemm_workgroups(args));
-    static const char* const names[3][3][3] = {
+    static const char* const names[5][3][3] = {
         {{"gemm_f32_mfma<K,K>", "gemm_f32_mfma<K,MN>", "gemm_f32_mfma<K,S>"},
          {"gemm_f32_mfma<MN,K>", "gemm_f32_mfma<MN,MN>", "gemm_f32_mfma<MN,S>"},
          {"gemm_f32_mfma<S,K>", "gemm_f32_mfma<S,MN>", "gemm_f32_mfma<S,S>"}},
@@ -295,8 +367,14 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
          {"gemm_f32_small<S,K>", "gemm_f32_small<S,MN>", "gemm_f32_small<S,S>"}},
         {{"gemm_f32_wave<K,K>", "gemm_f32_wave<K,MN>", "gemm_f32_wave<K,S>"},
          {"gemm_f32_wave<MN,K>", "gemm_f32_wave<MN,MN>", "gemm_f32_wave<MN,S>"},
-         {"gemm_f32_wave<S,K>", "gemm_f32_wave<S,MN>", "gemm_f32_wave<S,S>"}}};
-    if (args.kernel > KERN_WAVE) fail_invalid("unknown GEMM kernel");
+         {"gemm_f32_wave<S,K>", "gemm_f32_wave<S,MN>", "gemm_f32_wave<S,S>"}},
+        {{"gemm_f32_outer", "gemm_f32_outer", "gemm_f32_outer"},
+         {"gemm_f32_outer", "gemm_f32_outer", "gemm_f32_outer"},
+         {"gemm_f32_outer", "gemm_f32_outer", "gemm_f32_outer"}},
+        {{"gemm_f32_dl<K,K>", "gemm_f32_dl<K,MN>", "gemm_f32_dl<K,S>"},
+         {"gemm_f32_dl<MN,K>", "gemm_f32_dl<MN,MN>", "gemm_f32_dl<MN,S>"},
+         {"gemm_f32_dl<S,K>", "gemm_f32_dl<S,MN>", "gemm_f32_dl<S,S>"}}};
+    if (args.kernel > KERN_DIRECT) fail_invalid("unknown GEMM kernel");
 #define LG_GEMM_CASE(AMV, BMV)                       \
     if (a_mode == AMV && b_mode == BMV) {            \
         launch_gemm_t<AMV, BMV>(s, args, groups);    \
@@ -349,12 +427,11 @@ void launch_dot(Context* ctx, hipStream_t s, const DotArgs& args, bool vec) {
     }
     check_launch("dot_f32 launch");
     note_launch(ctx, "dot_f32");
-}
-
-void launch_clear_words(Context* ctx, hipStream_t s, uint32_t* p, uint64_t words) {
-    hipLaunchKernelGGL(clear_words, dim3(grid_for(words)), dim3(256), 0, s, p, words);
-    check_launch("clear_words launch");
-    note_launch(ctx, "clear_words");
+    if (args.splits > 1) {
+        hipLaunchKernelGGL(dot_finish_f32, dim3(args.batch), dim3(DOT_THREADS), 0, s, args);
+        check_launch("dot_finish_f32 launch");
+        note_launch(ctx, "dot_finish_f32");
+    }
 }
 
 void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args) {

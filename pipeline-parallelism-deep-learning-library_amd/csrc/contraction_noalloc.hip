@@ -1,17 +1,16 @@
 // lg_encode_gemm_f32_noalloc: lg_encode_gemm_f32 for callers that may not allocate device
 // memory (code under HIP graph capture, tight serving loops, harnesses that forbid it).
 //
-// Its split-K partials and dot-product tickets live in `scratch`, a file-scope device array of
-// SCRATCH_BYTES (16 KiB of ticket words + 32 MiB of partials, the most any plan uses: the
-// planner caps split counts to fit), which each GPU holds from the library's first use on it
-// until the process ends. In host code the array's name is only a stand-in: its device address
-// on each GPU is looked up once per device with hipGetSymbolAddress, on the entry point's first
-// call there, and only that address is handed to kernels. The same first call clears the
-// ticket words with a kernel on the caller's stream (a kernel, so the call may be captured),
-// and every call leaves them at zero again. Every call on one GPU shares that GPU's array, so
-// calls that overlap on one GPU (several streams, several contexts, or graph replays running
-// at once) race on it: the caller orders them. Nothing here allocates: no hipMalloc, no
-// hipFree, no allocating library routine.
+// Its split-K and split-dot partials live in `scratch`, a file-scope device array of
+// SCRATCH_BYTES (32 MiB, the most any plan uses: the planner caps split counts to fit), which
+// each GPU holds from the library's first use on it until the process ends. In host code the
+// array's name is only a stand-in: its device address on each GPU is looked up once per device
+// with hipGetSymbolAddress, on the entry point's first call there, and only that address is
+// handed to kernels. Every partial is written before it is read within one call, so nothing
+// needs clearing. Every call on one GPU shares that GPU's array, so calls that overlap on one
+// GPU (several streams, several contexts, or graph replays running at once) race on it: the
+// caller orders them. Nothing here allocates: no hipMalloc, no hipFree, no allocating library
+// routine.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -22,15 +21,15 @@ namespace lg {
 namespace {
 
 static_assert(SCRATCH_BYTES % 256 == 0, "scratch is whole 256-byte granules");
-static __device__ __align__(256) uint32_t scratch[SCRATCH_BYTES / sizeof(uint32_t)];
+static __device__ __align__(256) float scratch[SCRATCH_BYTES / sizeof(float)];
 
 constexpr int MAX_DEVICES = 64;
 std::mutex table_lock;
 void* table[MAX_DEVICES] = {};  // device address of `scratch` on each device, once looked up
 
-// The device address of `scratch` on the context's device (current when called), looked up and
-// its tickets cleared on `s` the first time.
-uint32_t* scratch_on(lg_ctx* ctx, hipStream_t s) {
+// The device address of `scratch` on the context's device (current when called), looked up
+// the first time.
+float* scratch_on(lg_ctx* ctx) {
     const int device = ctx->device;
     if (device < 0 || device >= MAX_DEVICES) fail_invalid("device index beyond the scratch table");
     std::lock_guard<std::mutex> hold(table_lock);
@@ -38,10 +37,9 @@ uint32_t* scratch_on(lg_ctx* ctx, hipStream_t s) {
         void* ptr = nullptr;
         check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         if (ptr == nullptr) fail_kernel("hipGetSymbolAddress(scratch) returned no address");
-        launch_clear_words(ctx, s, static_cast<uint32_t*>(ptr), TICKET_WORDS);
         table[device] = ptr;
     }
-    return static_cast<uint32_t*>(table[device]);
+    return static_cast<float*>(table[device]);
 }
 
 }  // namespace
@@ -54,7 +52,6 @@ extern "C" lg_status lg_encode_gemm_f32_noalloc(lg_ctx* ctx, void* stream, float
                                                 const lg_view* c) {
     return guarded([&] {
         if (ctx == nullptr) fail_invalid("null context");
-        enqueue_gemm_fixed_scratch(ctx, stream, alpha, a, b, beta, c, SCRATCH_BYTES - TICKET_BYTES,
-                                   scratch_on);
+        enqueue_gemm_fixed_scratch(ctx, stream, alpha, a, b, beta, c, SCRATCH_BYTES, scratch_on);
     });
 }

@@ -3,7 +3,9 @@
 // gemm_f32_mfma<AM, BMD, BK, TM, TN>: C = beta * C + sum_k (alpha * a) * b (or raw split-K
 // partials of the sum) for one stride per group. A (64*TM) x (64*TN) output tile per
 // 256-thread workgroup (4 waves in 2x2, each wave TM x TN blocks of v_mfma_f32_32x32x2_f32
-// accumulating in fp32); the product uses 128x128 and, for small grids, 64x64. K advances BK at a
+// accumulating in fp32); the library uses it for 64x64 tiles and for 128x128 tiles of
+// operands without a 16-byte aligned unit-stride axis (the others take gemm_f32_dl, with
+// slices loaded straight into LDS; gemm_dlds.h). K advances BK at a
 // time through two LDS stages: while the MFMAs consume stage s, the next K-slice is already in
 // flight from HBM into registers, and is written to stage s^1 before the one barrier per
 // slice. Operand loads follow the operand's unit-stride axis so a transposed or permuted
@@ -175,16 +177,10 @@ __device__ inline void mfma_group(floatx16 (&acc)[TM][TN], const floatx4 (&av)[T
                                                                  0, 0, 0);
 }
 
-// TM x TN blocks of 32x32 per wave, waves in 2x2: the workgroup tile is (64*TM) x (64*TN).
-// AHEAD = false: the next K-slice is requested at the top of a slice and written to LDS after
-// the slice's MFMAs; four waves per SIMD. AHEAD = true: the next slice is written to LDS right
-// after the first MFMA group (its stage was released by the previous barrier) and the slice
-// after it is requested there, two slices ahead; interior slices run a loop body with no
-// branch, so loads, LDS writes, fragment reads and MFMAs share one scheduling region; two
-// waves per SIMD. (Measured on MI355X: AHEAD is 5% faster when A is read along M, the
-// transposed-A product of a linear layer's weight gradient, and 1-2% slower otherwise.)
-template <int AM, int BMD, int BK, int TM, int TN, bool AHEAD = false>
-__global__ __launch_bounds__(GEMM_THREADS, (AM == LOAD_S || BMD == LOAD_S) ? 1 : (AHEAD ? 2 : 4))
+// TM x TN blocks of 32x32 per wave, waves in 2x2: the workgroup tile is (64*TM) x (64*TN). The
+// next K-slice is requested at the top of a slice and written to LDS after the slice's MFMAs.
+template <int AM, int BMD, int BK, int TM, int TN>
+__global__ __launch_bounds__(GEMM_THREADS, (AM == LOAD_S || BMD == LOAD_S) ? 1 : 4)
 void gemm_f32_mfma(GemmArgs p) {
     static_assert(TM * TN <= 4, "the occupancy bound assumes at most 2x2 blocks per wave");
     constexpr int TBM = 64 * TM, TBN = 64 * TN;
@@ -261,52 +257,13 @@ void gemm_f32_mfma(GemmArgs p) {
     load(0);
     store_slice<AM, BK, TBM, true>(As, ra, tid, alpha_a);
     store_slice<BMD, BK, TBN, true>(Bs, rb, tid, alpha_b);
-    if constexpr (AHEAD) {
-        if (ktiles > 1) load(BK);
-    }
     __syncthreads();
 
-    // With AHEAD, entering slice kt: LDS stage kt & 1 holds slice kt and the registers hold
-    // slice kt + 1.
     uint32_t kt = 0;
-    if constexpr (AHEAD) {
-        static_assert(AM != LOAD_S && BMD != LOAD_S, "the branch-free loop takes 128-bit loads");
-        // Interior tiles: every slice whose follower two ahead is a complete slice.
-        if (inner) {
-            const uint32_t full = klen / BK;
-            for (; kt + 2 < full; ++kt) {
-                const int s = kt & 1;
-                const float* as = As + s * A_ST;
-                const float* bs = Bs + s * B_ST;
-#pragma unroll
-                for (int g = 0; g < GROUPS; ++g) {
-                    floatx4 av[TM], bv[TN];
-                    read_frag<AM, BK, TBM, TM>(av, as, wm * 32 * TM, g, lr, h);
-                    read_frag<BMD, BK, TBN, TN>(bv, bs, wn * 32 * TN, g, lr, h);
-                    mfma_group<TM, TN>(acc, av, bv);
-                    if (g == 0) {
-                        store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
-                        store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
-                        const uint32_t k0 = (kt + 2) * BK;
-                        const int64_t oa = AM == LOAD_MN ? static_cast<int64_t>(k0) * p.a_sk : k0;
-                        const int64_t ob = BMD == LOAD_MN ? static_cast<int64_t>(k0) * p.b_sk : k0;
-#pragma unroll
-                        for (int i = 0; i < GA::LOADS; ++i) ra[i] = *reinterpret_cast<const floatx4*>(pa[i] + oa);
-#pragma unroll
-                        for (int i = 0; i < GB::LOADS; ++i) rb[i] = *reinterpret_cast<const floatx4*>(pb[i] + ob);
-                    }
-                }
-                __syncthreads();
-            }
-        }
-    }
-
     for (; kt < ktiles; ++kt) {
         const int s = kt & 1;
         const bool more = kt + 1 < ktiles;
-        if constexpr (!AHEAD) {
-            if (more) load((kt + 1) * BK);
-        }
+        if (more) load((kt + 1) * BK);
         const float* as = As + s * A_ST;
         const float* bs = Bs + s * B_ST;
         __builtin_amdgcn_s_setprio(1);
@@ -316,22 +273,11 @@ void gemm_f32_mfma(GemmArgs p) {
             read_frag<AM, BK, TBM, TM>(av, as, wm * 32 * TM, g, lr, h);
             read_frag<BMD, BK, TBN, TN>(bv, bs, wn * 32 * TN, g, lr, h);
             mfma_group<TM, TN>(acc, av, bv);
-            if constexpr (AHEAD) {
-                if (g == 0) {
-                    if (more) {
-                        store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
-                        store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
-                    }
-                    if (kt + 2 < ktiles) load((kt + 2) * BK);
-                }
-            }
         }
         __builtin_amdgcn_s_setprio(0);
-        if constexpr (!AHEAD) {
-            if (more) {
-                store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
-                store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
-            }
+        if (more) {
+            store_slice<AM, BK, TBM, true>(As + (s ^ 1) * A_ST, ra, tid, alpha_a);
+            store_slice<BMD, BK, TBN, true>(Bs + (s ^ 1) * B_ST, rb, tid, alpha_b);
         }
         __syncthreads();
     }

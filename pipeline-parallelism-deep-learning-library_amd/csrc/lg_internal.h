@@ -72,9 +72,9 @@ struct Context {
     std::mutex mse_lock;
     void* mse_scratch = nullptr;
     float* mse_host = nullptr;
-    // Split-K partials and the dot path's tickets: one buffer per context, SCRATCH_BYTES long,
-    // allocated with the context (its ticket words zeroed) and never grown, so a split call
-    // never allocates or synchronizes -- also under stream capture. split_lock is held while
+    // Split-K and split-dot partials: one buffer per context, SCRATCH_BYTES long, allocated
+    // with the context and never grown, so a split call never allocates or synchronizes --
+    // also under stream capture. split_lock is held while
     // a call hands the buffer to its launches. Calls on one stream are ordered by the stream;
     // an eager call on another stream first waits for split_event, which marks the end of the
     // previous user's work.
@@ -138,8 +138,13 @@ constexpr uint32_t GEMM_THREADS = 256;
 enum GemmKernel : uint32_t {
     KERN_TILE = 0,   // gemm_f32_mfma: 128x128 (or 64x64) tile per 256-thread workgroup
     KERN_SMALL = 1,  // gemm_f32_small: one 32x32 tile per workgroup, sixteen waves split K
-    KERN_WAVE = 2    // gemm_f32_wave: one 32x32 tile per wave, four tiles per workgroup
+    KERN_WAVE = 2,   // gemm_f32_wave: one 32x32 tile per wave, four tiles per workgroup
+    KERN_OUTER = 3,  // outer_f32: K <= OUTER_MAX_K on the VALU, four outputs per thread
+    KERN_DIRECT = 4  // gemm_f32_dl: 128x128 or 128x256 tiles, slices loaded straight into LDS
 };
+// N extent of the wide direct-load tile (eight waves, 128x256).
+constexpr uint32_t GEMM_WIDE_N = 256;
+constexpr uint32_t OUTER_MAX_K = 8;
 
 struct GemmArgs {
     const float* a;  // element pointer of A's view offset
@@ -153,23 +158,26 @@ struct GemmArgs {
     uint32_t k_chunk, splits;
     uint32_t tiles_m, tiles_n;
     float alpha, beta;
-    uint32_t tile;     // output tile edge: GEMM_BM (128), GEMM_SMALL_TILE (64) or GEMM_TINY_TILE (32)
+    uint32_t tile;     // output tile edge along M: 128, 64 or 32 (1 for KERN_OUTER)
+    uint32_t tile_n;   // along N: `tile`, or GEMM_WIDE_N for the wide direct-load tile
     uint32_t kernel;   // GemmKernel
     // 0: alpha scales the A-role operand as it is loaded; 1: the B-role one. The planner swaps
     // the operands (C^T = B^T.A^T) when C is contiguous along M, and the operand it then
     // loads as B is the caller's A: every product stays (alpha*a)*b.
     uint32_t scale_b;
+    // KERN_OUTER: 1 when C is contiguous along N, n % 4 == 0 and every row 16-byte aligned
+    // (128-bit stores), and (vec_b) the same for B (128-bit loads).
+    uint32_t vec_c, vec_b;
 };
 
 // Dot products (M = N = 1): C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k]. Split along K
-// into `splits` workgroups per product, whose partial sums the last one to finish (a ticket
-// per product) adds in split order.
+// into `splits` workgroups per product writing partial sums, which a second launch adds in
+// split order.
 struct DotArgs {
     const float* a;
     const float* b;
     float* c;
     float* partial;     // [batch][splits] when splits > 1
-    uint32_t* tickets;  // [batch] zeroed words when splits > 1; each is zero again afterwards
     int64_t a_sb, a_sk, b_sb, b_sk, c_sb;
     uint32_t k, batch, k_chunk, splits;
     float alpha, beta;
@@ -179,12 +187,10 @@ constexpr uint32_t DOT_THREADS = 256;
 constexpr uint32_t DOT_MIN_CHUNK = 4096;   // K elements per split, at least
 constexpr uint32_t DOT_TARGET = 2048;      // workgroups the split dot path aims for
 
-// The per-context scratch: TICKET_WORDS ticket words, then split partials. Plans never need
-// more partial bytes than SPLIT_PARTIAL_MAX (the planner caps the split count to fit).
-constexpr uint64_t TICKET_WORDS = 4096;
-constexpr uint64_t TICKET_BYTES = TICKET_WORDS * 4;
+// The per-context scratch of split partials. Plans never need more than SPLIT_PARTIAL_MAX
+// bytes of partials (the planner caps the split count to fit).
 constexpr uint64_t SPLIT_PARTIAL_MAX = 32ull << 20;
-constexpr uint64_t SCRATCH_BYTES = TICKET_BYTES + SPLIT_PARTIAL_MAX;
+constexpr uint64_t SCRATCH_BYTES = SPLIT_PARTIAL_MAX;
 
 struct ReduceArgs {
     const float* partial;
@@ -255,9 +261,8 @@ uint64_t gemm_half_workgroups(uint32_t m, uint32_t n, uint32_t batch);
 
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode);
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args);
+// The dot kernel, then (split dots) the ordered sum of the partials.
 void launch_dot(Context* ctx, hipStream_t s, const DotArgs& args, bool vec);
-// Clears `words` 32-bit words with a kernel (graph-capturable, unlike hipMemsetAsync).
-void launch_clear_words(Context* ctx, hipStream_t s, uint32_t* p, uint64_t words);
 void launch_general(Context* ctx, hipStream_t s, const GeneralArgs& args);
 void launch_fill(Context* ctx, hipStream_t s, const FillArgs& args);
 uint64_t gemm_workgroups(const GemmArgs& args);
@@ -342,12 +347,12 @@ void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, 
                         float beta, const View& c, uint32_t dtype);
 // Plans C = alpha*A.B + beta*C (the gemm form, f32) and enqueues it on `stream` with device
 // scratch from the caller: once validation and planning have passed, and only when the plan
-// needs scratch, `scratch(ctx, s)` is called with the context's device current and returns
-// TICKET_WORDS ticket words that are zero, followed by `partial_cap` bytes for split partials.
-// A plan needing more than partial_cap fails with InvalidArgument before anything is launched.
+// needs scratch, `scratch(ctx)` is called with the context's device current and returns
+// `partial_cap` bytes of device memory for split partials. A plan needing more than
+// partial_cap fails with InvalidArgument before anything is launched.
 void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
                                 const lg_view* b, float beta, const lg_view* c,
-                                uint64_t partial_cap, uint32_t* (*scratch)(lg_ctx*, hipStream_t));
+                                uint64_t partial_cap, float* (*scratch)(lg_ctx*));
 inline hipStream_t pick_stream(const lg_ctx* ctx, void* stream) {
     return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 }

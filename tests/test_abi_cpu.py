@@ -215,9 +215,12 @@ def dense(shape, **kw):
 
 
 def test_output_tile_choice():
-    # 17 x 17 = 289 tiles of 128x128: the large tile; 15 x 16 = 240: 64x64 (30 x 31 of them).
+    # 17 x 17 = 289 tiles of 128x128 put two on some compute units and one on most: 64x64
+    # (33 x 33 of them); 16 x 16 = 256 spread evenly: the large tile; 15 x 16 = 240: 64x64.
     p = C.plan_gemm(1.0, dense([2100, 37]), dense([37, 2050]), 0.0, dense([2100, 2050]))
-    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (128, 128), 289)
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (64, 64), 33 * 33)
+    p = C.plan_gemm(1.0, dense([2048, 37]), dense([37, 2048]), 0.0, dense([2048, 2048]))
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (128, 128), 256)
     p = C.plan_gemm(1.0, dense([1900, 45]), dense([45, 1950]), 0.0, dense([1900, 1950]))
     assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (64, 64), 30 * 31)
     # Small output, short K: one launch of 32x32 tiles.
@@ -235,13 +238,13 @@ def test_output_tile_choice():
 def test_contraction_plans_for_the_reference_benchmark_shapes():
     """The shapes of tests/contraction_test.rs:1293-1395 (bench_other_paths): no output is padded
     past half of its tiles, C stored column-major is computed as C^T = B^T.A^T, and dot products
-    run on the VALU."""
+    and K <= 8 updates run on the VALU."""
     t = lambda r, c: view(Layout.transposed(r, c))
     # "transposed 2048": A, B and C all column-major.
     p = C.plan_contract(1.0, (t(2048, 2048), "mk"), (t(2048, 2048), "kn"), 0.0,
                         (t(2048, 2048), "mn"))
     assert p["swapped"] and (p["a_mode"], p["b_mode"]) == ("k", "mn")
-    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "tile", (128, 128), 256)
+    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "direct", (128, 128), 256)
     # "batched 4096 x 32^3": one 32x32 tile per wave, four per workgroup.
     p = C.plan_contract(1.0, (dense([4096, 32, 32]), "bmk"), (dense([4096, 32, 32]), "bkn"), 0.0,
                         (dense([4096, 32, 32]), "bmn"))
@@ -259,12 +262,16 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     assert (p["a_mode"], p["b_mode"]) == ("k", "k") and p["workgroups"] == p["splits"] == 512
     assert p["scratch_bytes"] == 512 * 32 * 32 * 4 <= 32 << 20
     # "rank-1 4096^2" and "rank-4 ijkl,klmn->ijmn 48^6" (axes merge to a 2304^3 product).
+    # K <= 8 runs on the VALU in crates/cpu's own order, four outputs per thread.
     p = C.plan_contract(1.0, (dense([4096, 1]), "mk"), (dense([1, 4096]), "kn"), 0.0,
                         (dense([4096, 4096]), "mn"))
-    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (128, 128), 1024)
+    assert (p["kind"], p["kernel"], p["tile"], p["b_mode"]) == ("tiled", "outer", (1, 4), "mn")
+    assert p["workgroups"] == 2048  # a grid-stride loop over the 4096 * 1024 quads
     p = C.plan_contract(1.0, (dense([48] * 4), "ijkl"), (dense([48] * 4), "klmn"), 0.0,
                         (dense([48] * 4), "ijmn"))
     assert (p["kind"], p["groups"], p["m"], p["n"], p["k"]) == ("tiled", 1, 2304, 2304, 2304)
+    # 324 tiles of 128x128 spread unevenly over 256 compute units: 64x64 tiles (1296).
+    assert (p["tile"], p["workgroups"]) == ((64, 64), 1296)
     # Batched dot products (no split once the batch fills the chip) and a skinny output.
     p = C.plan_contract(1.0, (dense([4096, 1, 512]), "bmk"), (dense([4096, 512, 1]), "bkn"), 0.0,
                         (dense([4096, 1, 1]), "bmn"))
@@ -287,11 +294,13 @@ def test_contraction_plans_for_the_baseline_configs():
     p = C.plan_contract(1.0, (dense([32, 1024, 1024]), "bik"), (bview, "bkj"), 0.0,
                         (dense([32, 1024, 1024]), "bij"))
     assert p["kind"] == "tiled" and p["batch"] == 32 and p["b_mode"] == "k" and p["a_mode"] == "k"
-    assert p["tile"] == (128, 128)
+    # 1024 tiles of 128x256 fill the chip: the wide direct-load tile.
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("direct", (128, 256), 32 * 8 * 4)
     # Config 4: tall K goes split-K with a fixed chunk grid.
     p = C.plan_gemm(1.0, dense([256, 65536]), dense([65536, 256]), 0.0, dense([256, 256]))
     assert p["kind"] == "split" and p["splits"] > 1 and p["k_chunk"] % 32 == 0
-    assert p["tile"] == (128, 128)  # split-K alone fills the chip: keep the large tile
+    # Split-K alone fills the chip: 128x128 direct-load tiles, split along K.
+    assert (p["kernel"], p["tile"]) == ("direct", (128, 128))
     assert p["splits"] * p["k_chunk"] >= 65536 > (p["splits"] - 1) * p["k_chunk"]
     assert p["scratch_bytes"] == p["splits"] * 256 * 256 * 4
     # Config 5: transpose_matrix views (strides [1, rows]) are read in place.
@@ -299,7 +308,7 @@ def test_contraction_plans_for_the_baseline_configs():
     Wt = L.TensorView(W.buffer, 0, [16384, 4096], [1, 16384])
     Xt = L.TensorView(X.buffer, 0, [4096, 4096], [1, 4096])
     p = C.plan_gemm(1.0, X, W, 0.0, dense([4096, 16384]))
-    assert p["kind"] == "tiled" and p["tile"] == (128, 128) and p["workgroups"] == 32 * 128
+    assert p["kind"] == "tiled" and p["tile"] == (128, 256) and p["workgroups"] == 32 * 64
     p = C.plan_gemm(1.0, dY, Wt, 0.0, dense([4096, 4096]))
     assert (p["a_mode"], p["b_mode"]) == ("k", "k")
     p = C.plan_gemm(1.0, Xt, dY, 1.0, dense([4096, 16384]))

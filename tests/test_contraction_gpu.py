@@ -493,13 +493,13 @@ def test_both_output_tiles_on_ragged_edges(ctx, pool):
         seed += 1
 
 
-def test_transposed_a_two_ahead_pipeline(ctx, pool):
-    """A read along M (transpose_matrix(X), the weight-gradient operand) takes the 128x128
-    kernel's two-slices-ahead pipeline: K with no complete follower slice, a branch-free
-    interior run followed by the general tail (partial last slice), exact slices, ragged
-    M/N edge tiles, split-K chunks, and both B layouts, against both oracles."""
+def test_transposed_a_direct_load_pipeline(ctx, pool):
+    """A read along M (transpose_matrix(X), the weight-gradient operand) through the 128x128
+    direct-load kernel's three-stage pipeline: K shorter than the pipeline, full slices followed
+    by a partial last slice loaded through registers, exact slices, ragged M/N edge tiles (loaded
+    through registers), split-K chunks, and both B layouts, against both oracles."""
     seed = 6200
-    cases = [((2100, 2050, 37), (False,)), ((2080, 2050, 147), (False, True)),
+    cases = [((3000, 2050, 37), (False,)), ((3000, 2060, 147), (False, True)),
              ((2048, 2048, 96), (False,)), ((400, 300, 8192), (False, True))]
     for (m, n, k), b_layouts in cases:
         for tb in b_layouts:
@@ -510,13 +510,16 @@ def test_transposed_a_two_ahead_pipeline(ctx, pool):
             plan = C.plan_gemm(alpha, _dummy_view(pool, case.a[0]), _dummy_view(pool, case.b[0]),
                                beta, _dummy_view(pool, case.c[0]))
             assert plan["tile"] == (128, 128) and plan["a_mode"] == "mn", plan
+            # A B row pitch off a multiple of four elements has no 16-byte aligned unit-stride
+            # axis: the register-staged kernel; every other case loads slices straight into LDS.
+            assert plan["kernel"] == ("tile" if plan["b_mode"] == "strided" else "direct"), plan
             case.scalars(alpha, beta).run(ctx, pool, seed)
             pool.free_all()
             seed += 1
 
 
 def test_transposed_a_pipeline_batched(ctx, pool):
-    """Batched products whose A is read along M take the same two-ahead kernel per batch
+    """Batched products whose A is read along M take the same direct-load kernel per batch
     plane: four 1024x1024x256 planes (256 tiles of 128x128, no split-K)."""
     b, m, n, k = 4, 1024, 1024, 256
     case = Case("batched A^T", (Layout.with_([b, m, k], [0, 2, 1], [1, 1, 1], 0), "bmk"),
@@ -530,7 +533,7 @@ def test_transposed_a_pipeline_batched(ctx, pool):
 
 
 def test_transposed_a_pipeline_is_deterministic(ctx, pool):
-    """The two-ahead pipeline with split-K chunks (A read along M) gives the same bits on
+    """The direct-load pipeline with split-K chunks (A read along M) gives the same bits on
     three runs, with beta = 1 accumulating into the same starting C each time."""
     m, n, k = 400, 300, 8192
     g = rng(6300)
@@ -715,3 +718,60 @@ def test_gemm_nowait_is_ordered_before_a_download(ctx, pool, m, n, k):
     ref2 = np.zeros(m * n, np.float32)
     oracle.gemm_fast(m, n, n, 1.0, 0.0, c2, 0, (n, 1), sq, 0, (n, 1), ref2, 0, (n, 1))
     _rows_check("gemm_nowait D", d, ref2, n, float(np.abs(c2).max()), 1.0)
+
+
+def _gemm_fast_check(name, got_buf, a, la, b, lb, c0, lc, m, n, k, alpha, beta):
+    """Every element of C (layout lc inside got_buf) against the crates/cpu restatement."""
+    ref = c0.copy()
+    oracle.gemm_fast(m, n, k, alpha, beta, a, la.offset, la.strides, b, lb.offset, lb.strides,
+                     ref, lc.offset, lc.strides)
+    idx = (lc.offset + np.arange(m)[:, None] * lc.strides[0] +
+           np.arange(n)[None, :] * lc.strides[1]).ravel()
+    tol = 1e-5 * np.sqrt(k) * abs(alpha) + (1e-5 * abs(beta) if beta != 0.0 else 0.0)
+    err = np.abs(got_buf[idx].astype(np.float64) - ref[idx].astype(np.float64))
+    assert np.all(np.isfinite(got_buf[idx])) and float(err.max()) <= tol, (name, float(err.max()), tol)
+
+
+@pytest.mark.parametrize("ta,tb,tc", [(False, False, False), (True, False, False), (False, True, False),
+                                      (True, True, False), (False, False, True)])
+def test_wide_direct_load_tiles_with_ragged_edges(ctx, pool, ta, tb, tc):
+    """128x256 direct-load tiles (grids of at least 512 of them): ragged M and N edge tiles and a
+    partial last K-slice (both loaded through registers), every operand layout pair, and C
+    stored column-major (computed transposed), against crates/cpu on every element."""
+    m, n, k = 4100, 4100, 1000
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(7300 + 4 * ta + 2 * tb + tc)
+    alpha, beta = (1.0, 0.0) if not (ta or tb) else (-0.75, 0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kernel"], plan["tile"]) == ("direct", (128, 256)), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    _gemm_fast_check(f"wide ta={ta} tb={tb} tc={tc}", Cc.read(), A.host, la, B.host, lb, c0, lc,
+                     m, n, k, alpha, beta)
+
+
+def test_wide_direct_load_batched_with_permuted_b(ctx, pool):
+    """Eight 1100x2100x300 planes with B a permuted view (unit stride along K), beta = 1: 648
+    wide tiles, ragged in M and N."""
+    bsz, m, n, k = 8, 1100, 2100, 300
+    g = rng(7400)
+    a = g.uniform(-1, 1, bsz * m * k).astype(np.float32)
+    bstore = g.uniform(-1, 1, bsz * n * k).astype(np.float32)  # [b, n, k]
+    c0 = g.uniform(-1, 1, bsz * m * n).astype(np.float32)
+    A = Tensor(pool, Layout.dense([bsz, m, k]), a)
+    Bs = Tensor(pool, Layout.dense([bsz, n, k]), bstore)
+    Cc = Tensor(pool, Layout.dense([bsz, m, n]), c0)
+    bview = P.permute_view(Bs.view(), [0, 2, 1])
+    plan = C.plan_contract(0.5, (A.view(), "bik"), (bview, "bkj"), 1.0, (Cc.view(), "bij"))
+    assert (plan["kernel"], plan["tile"], plan["b_mode"]) == ("direct", (128, 256), "k"), plan
+    C.contract(ctx, 0.5, (A.view(), "bik"), (bview, "bkj"), 1.0, (Cc.view(), "bij"))
+    got = Cc.read()
+    for bi in range(bsz):
+        ref = c0[bi * m * n:(bi + 1) * m * n].copy()
+        oracle.gemm_fast(m, n, k, 0.5, 1.0, a, bi * m * k, (k, 1), bstore, bi * n * k, (1, k),
+                         ref, 0, (n, 1))
+        err = np.abs(got[bi * m * n:(bi + 1) * m * n].astype(np.float64) - ref.astype(np.float64))
+        assert float(err.max()) <= 1e-5 * np.sqrt(k) * 0.5 + 1e-5, (bi, float(err.max()))

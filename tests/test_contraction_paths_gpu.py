@@ -5,7 +5,8 @@
   long K), partials added in a fixed order,
 * dot products on the VALU (M = N = 1), split along K, the partials added in order by the
   workgroup that draws the last ticket,
-* C stored contiguous along M, computed as C^T = B^T.A^T (alpha still scales A's elements).
+* C stored contiguous along M, computed as C^T = B^T.A^T (alpha still scales A's elements),
+* K <= 8 on the VALU in the reference's own order, bit for bit against crates/cpu.
 
 Small cases run through helpers.Case (the f64 reference of tests/contraction_test.rs:200-268
 with its gate, the crates/cpu restatement with the north-star bound for 2-D gemm, and every
@@ -39,7 +40,7 @@ def plan_of(case: Case, pool):
 # one tile per wave
 # --------------------------------------------------------------------------------------
 @pytest.mark.parametrize("bsz,m,n,k", [(1024, 32, 32, 32), (1100, 17, 31, 9), (1030, 33, 20, 45),
-                                       (600, 40, 50, 3), (2048, 8, 8, 100)])
+                                       (600, 40, 50, 12), (2048, 8, 8, 100)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (-1.25, 0.5)])
 def test_batched_small_products_one_tile_per_wave(ctx, pool, bsz, m, n, k, alpha, beta):
     case = Case(f"batched {bsz}x{m}x{n}x{k}", (dense([bsz, m, k]), "bmk"), (dense([bsz, k, n]), "bkn"),
@@ -152,6 +153,36 @@ def test_dot_split_tickets_stay_consistent_across_calls(ctx, pool):
                 assert np.max(np.abs(got - np.array(ref))) <= 1e-5 * np.sqrt(k), (bsz, k)
             else:
                 assert np.array_equal(got.view(np.uint32), outs[(bsz, k)].view(np.uint32)), (bsz, k)
+
+
+# --------------------------------------------------------------------------------------
+# K <= 8: the VALU in crates/cpu's own order, bit for bit
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("k", [1, 2, 5, 8])
+@pytest.mark.parametrize("m,n", [(1, 7), (33, 64), (130, 257), (4, 1000)])
+@pytest.mark.parametrize("layout", ["rm", "c_cm", "b_strided"])
+def test_low_rank_updates_equal_crates_cpu_bit_for_bit(ctx, pool, k, m, n, layout):
+    """acc = beta == 0 ? +0 : beta*C, then acc += (alpha*a)*b in k order: the reference's loop
+    (crates/cpu/src/lib.rs:664-691), so every output equals oracle.gemm_seq's bits."""
+    g = rng(k * 1000 + m + n)
+    la = Layout.dense([m, k])
+    lb = Layout.with_([k, n], [0, 1], [1, 3], 1) if layout == "b_strided" else Layout.dense([k, n])
+    lc = Layout.transposed(m, n) if layout == "c_cm" else Layout.dense([m, n])
+    for alpha, beta in [(1.0, 0.0), (-1.5, 0.75), (0.3, 1.0)]:
+        a, b, c = (Tensor.random(pool, lay, g) for lay in (la, lb, lc))
+        if beta == 0.0:
+            c.host[:] = np.nan
+            c.upload()
+        a0, b0, c0 = a.host.copy(), b.host.copy(), c.host.copy()
+        plan = C.plan_gemm(alpha, a.view(), b.view(), beta, c.view())
+        assert (plan["kind"], plan["kernel"]) == ("tiled", "outer"), plan
+        C.gemm(ctx, alpha, a.view(), b.view(), beta, c.view())
+        ref = c0.copy()
+        oracle.gemm_seq(m, n, k, alpha, beta, a0, la.offset, la.strides, b0, lb.offset, lb.strides,
+                        ref, lc.offset, lc.strides)
+        got = c.read()
+        assert np.array_equal(got[: ref.size].view(np.uint32), ref.view(np.uint32)), (k, m, n, layout,
+                                                                                     alpha, beta)
 
 
 # --------------------------------------------------------------------------------------
@@ -273,8 +304,8 @@ def test_bench_rank1_4096(ctx, pool):
     c = Tensor(pool, dense([n, n]))
     C.contract(ctx, 1.0, (a.view(), "mk"), (b.view(), "kn"), 0.0, (c.view(), "mn"))
     got = c.read()[: n * n]
-    # One product per element: crates/cpu's +0 + (alpha*a)*b, exactly the f32 product (+0 for
-    # a zero product of either sign).
+    # K = 1 runs crates/cpu's loop: +0 + (alpha*a)*b, exactly the f32 product (+0 for a zero
+    # product of either sign).
     want = np.float32(0.0) + np.outer(x, y).astype(np.float32).ravel()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
