@@ -295,7 +295,7 @@ lg_core_error lg_backend_add_bias(lg_ctx* ctx, void* stream, const lg_tensor* x,
 
 /* bias_grad (crates/cpu/src/lib.rs:403-435): db[j] = db[j] + (dpre[0][j] + dpre[1][j] + ...),
  * rows summed in order as the reference does, so the result is the reference's bits.
- * Checks: Shape (dpre [B, N], db [N]), Dtype, Alias, layout, storage; B, N < 2^32. */
+ * Checks: Shape (dpre [B, N], db [N]), Dtype, Alias, layout, storage; B, N < 2^31. */
 lg_core_error lg_backend_bias_grad(lg_ctx* ctx, void* stream, const lg_tensor* dpre,
                                    const lg_tensor* db);
 
@@ -356,8 +356,11 @@ lg_core_error lg_wire_encode(uint32_t dtype, const uint64_t* shape, uint32_t ran
                              uint64_t out_cap, uint64_t* written);
 /* send_tensor's download + encode_wire (crates/pipeline/src/lib.rs:71-80) in one device-to-host
  * copy straight into the wire buffer: after every earlier call on the context stream, returns
- * when the bytes are final. The tensor must be row-major at offset 0 (else
- * LG_CORE_UNSUPPORTED_LAYOUT). Host-memory rate; no kernel runs. */
+ * when the bytes are final. Checks in the reference's order: the dtype tag (LG_CORE_WIRE);
+ * download's (crates/cpu/src/lib.rs:183-194): row-major strides at any offset (else
+ * LG_CORE_UNSUPPORTED_LAYOUT), the byte range inside the storage (else LG_CORE_SHAPE); then
+ * encode_wire's header checks (rank above 8: LG_CORE_WIRE; extent above u32::MAX: LG_CORE_SHAPE);
+ * `out_cap` too small: LG_CORE_SHAPE. Host-memory rate; no kernel runs. */
 lg_core_error lg_wire_encode_tensor(lg_ctx* ctx, const lg_tensor* t, uint8_t* out,
                                     uint64_t out_cap, uint64_t* written);
 /* recv_tensor's decode_wire + upload (crates/pipeline/src/lib.rs:82-98) into an existing tensor

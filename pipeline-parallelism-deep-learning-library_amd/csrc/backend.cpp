@@ -264,8 +264,10 @@ lg_core_error lg_backend_bias_grad(lg_ctx* ctx, void* stream, const lg_tensor* d
         if (dpre->base == db->base) core_fail(LG_CORE_ALIAS, "db shares storage with dpre");
         packed({dpre, db});
         const uint64_t rows = dpre->shape[0], cols = dpre->shape[1];
-        if (rows > 0xffffffffull || cols > 0xffffffffull) {
-            core_fail(LG_CORE_SHAPE, "bias_grad extents must fit 32 bits");
+        // The kernel walks rows in blocks with 32-bit arithmetic (rows + block - 1 must not
+        // wrap): extents are 31-bit.
+        if (rows > 0x7fffffffull || cols > 0x7fffffffull) {
+            core_fail(LG_CORE_SHAPE, "bias_grad extents must fit 31 bits");
         }
         hipStream_t s = device_stream(ctx, stream);
         if (rows > 0 && cols > 0) {

@@ -101,9 +101,11 @@ struct Gather {
     bool conj = false;
 };
 
+// Kernel extents are 31-bit: the tile kernels add a tile's extent to a coordinate in 32-bit
+// arithmetic, which must not wrap.
 uint32_t fit32(uint64_t x, const char* what) {
-    if (x > UINT32_MAX) fail_invalid(std::string(what) + " " + std::to_string(x) +
-                                     " does not fit 32-bit kernel extents");
+    if (x > 0x7fffffffull) fail_invalid(std::string(what) + " " + std::to_string(x) +
+                                        " does not fit 31-bit kernel extents");
     return static_cast<uint32_t>(x);
 }
 

@@ -100,9 +100,10 @@ uint64_t parse_header(const uint8_t* bytes, uint64_t len, uint32_t* tag, uint64_
     return header;
 }
 
-// Row-major contiguous at offset 0 (packed_layout, crates/cpu/src/lib.rs:735-747).
-bool packed_tensor(const lg_tensor* t) {
-    if (t->offset != 0 || t->nstrides != t->rank || t->rank > LG_MAX_RANK) return false;
+// strides == row_major_strides(shape) (crates/core/src/lib.rs:275-283); the running product
+// wraps as the reference's does in release builds.
+bool row_major_tensor(const lg_tensor* t) {
+    if (t->nstrides != t->rank || t->rank > LG_MAX_RANK) return false;
     uint64_t stride = 1;
     for (uint32_t d = t->rank; d-- > 0;) {
         if (t->strides[d] != stride) return false;
@@ -110,6 +111,9 @@ bool packed_tensor(const lg_tensor* t) {
     }
     return true;
 }
+
+// Row-major contiguous at offset 0 (packed_layout, crates/cpu/src/lib.rs:735-747).
+bool packed_tensor(const lg_tensor* t) { return t->offset == 0 && row_major_tensor(t); }
 
 template <typename F>
 lg_core_error wire_op(F&& body) {
@@ -190,18 +194,33 @@ lg_core_error lg_wire_encode_tensor(lg_ctx* ctx, const lg_tensor* t, uint8_t* ou
                                     uint64_t out_cap, uint64_t* written) {
     return wire_op([&] {
         if (t == nullptr || written == nullptr) wfail(LG_CORE_SHAPE, "null argument");
+        const uint64_t size = size_of(t->dtype);  // a Tensor's dtype is a DType: decode it first
         if (t->rank > LG_MAX_RANK) wfail(LG_CORE_SHAPE, "rank above LG_MAX_RANK");
-        if (!packed_tensor(t)) wfail(LG_CORE_UNSUPPORTED_LAYOUT, "tensor is not row-major at offset 0");
+        // Backend::download (crates/cpu/src/lib.rs:183-194): row-major strides at any offset,
+        // then the byte range [offset*size, offset*size + numel*size) inside the storage.
+        if (!row_major_tensor(t)) wfail(LG_CORE_UNSUPPORTED_LAYOUT, "tensor is not row-major");
+        uint64_t count = 1;
+        for (uint32_t d = 0; d < t->rank; ++d) {
+            if (t->shape[d] != 0 && count > UINT64_MAX / t->shape[d]) wfail(LG_CORE_SHAPE, "element count overflows");
+            count *= t->shape[d];
+        }
+        if (t->offset > UINT64_MAX / size) wfail(LG_CORE_SHAPE, "offset overflows");
+        if (count > UINT64_MAX / size) wfail(LG_CORE_SHAPE, "byte count overflows");
+        const uint64_t start = t->offset * size, len = count * size;
+        if (start > UINT64_MAX - len) wfail(LG_CORE_SHAPE, "byte range overflows");
+        if (start + len > t->bytes) wfail(LG_CORE_SHAPE, "tensor reaches past its storage");
+        // encode_wire (crates/core/src/lib.rs:309-322).
         uint8_t head[LG_WIRE_HEADER_MAX];
         uint64_t nbytes = 0;
         const uint64_t h = write_header(t->dtype, t->shape, t->rank, head, &nbytes);
-        if (nbytes > t->bytes) wfail(LG_CORE_SHAPE, "tensor reaches past its storage");
+        if (h > UINT64_MAX - nbytes) wfail(LG_CORE_SHAPE, "message length overflows");
         if (out == nullptr || out_cap < h + nbytes) wfail(LG_CORE_SHAPE, "output buffer too small");
         if (ctx == nullptr) wfail(LG_CORE_UNSUPPORTED_DEVICE, "null context");
         set_device(ctx);
         // After every earlier call on the context stream, like Backend::download.
         if (nbytes) {
-            check_hip(hipMemcpyAsync(out + h, t->base, nbytes, hipMemcpyDeviceToHost, ctx->stream),
+            const uint8_t* src = static_cast<const uint8_t*>(t->base) + start;
+            check_hip(hipMemcpyAsync(out + h, src, nbytes, hipMemcpyDeviceToHost, ctx->stream),
                       "hipMemcpyAsync");
         }
         check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");

@@ -210,6 +210,18 @@ def test_permutation_error_precedence():
         P.plan("materialize", big, view(Layout.dense([2] * 9)))
 
 
+def test_permutation_extents_are_31_bit():
+    """Tile-path extents up to 2^31 - 1 plan; 2^31 is refused before any launch."""
+    ok = (1 << 31) - 1
+    for dtype in ("f32", "c64"):
+        x = view(Layout.dense([2, ok]), dtype=dtype)
+        p = P.plan("materialize", P.permute_view(x, [1, 0]), view(Layout.dense([ok, 2]), dtype=dtype))
+        assert p["kind"] == "tile" and sorted(p["shape"]) == [2, ok]
+        x = view(Layout.dense([2, ok + 1]), dtype=dtype)
+        with pytest.raises(L.InvalidArgument, match="31-bit"):
+            P.plan("materialize", P.permute_view(x, [1, 0]), view(Layout.dense([ok + 1, 2]), dtype=dtype))
+
+
 def dense(shape, **kw):
     return view(Layout.dense(shape), **kw)
 

@@ -248,6 +248,14 @@ def test_training_op_errors_come_in_contract_order():
     assert op_kind("gelu", alias_of(x, dtype=7), y) == "Wire"
 
 
+def test_bias_grad_extents_are_31_bit():
+    ok = (1 << 31) - 1
+    with pytest.raises(B.BackendError, match="null context"):
+        B.op_checks("bias_grad", rm([ok, 1]), rm([1]))
+    assert op_kind("bias_grad", rm([ok + 1, 1]), rm([1])) == "Shape"
+    assert op_kind("bias_grad", rm([1, ok + 1]), rm([ok + 1])) == "Shape"
+
+
 def test_training_ops_pass_their_checks_on_valid_operands():
     x, b, y = rm([2, 3]), rm([3]), rm([2, 3])
     cases = [("gelu", x, y), ("gelu", x, alias_of(x)), ("gelu_backward", x, rm([2, 3]), y),

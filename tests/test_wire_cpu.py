@@ -148,3 +148,45 @@ def test_corrupted_and_random_messages_never_misparse():
         assert h[0] == dt and h[1] == shape and h[2] == len(t) - len(payload)
         ok += 1
     assert ok >= len(seeds)
+
+
+def encode_tensor_kind(t, out_cap=None) -> str:
+    """lg_wire_encode_tensor with no context: the first failing check, or UnsupportedDevice
+    ("null context") when every check passes. Storage bases are never dereferenced."""
+    import ctypes
+    from linalg_hip import _native as N
+    from linalg_hip.backend import _raise
+    cap = out_cap if out_cap is not None else W.WIRE_HEADER_MAX + t.numel() * t.dtype.size_of()
+    out = ctypes.create_string_buffer(max(cap, 1))
+    n = ctypes.c_uint64()
+    code = N.lib().lg_wire_encode_tensor(None, ctypes.byref(t.to_c()), out, cap, ctypes.byref(n))
+    with pytest.raises(BackendError) as e:
+        _raise(code)
+    return e.value.kind
+
+
+def test_encode_tensor_checks_in_download_then_encode_wire_order():
+    """send_tensor = download (crates/cpu/src/lib.rs:183-194) then encode_wire
+    (crates/core/src/lib.rs:309-322): layout, then the storage range, then the header."""
+    from linalg_hip.backend import Storage, Tensor, row_major_strides
+
+    def tensor(shape, nbytes, offset=0, strides=None, dtype=DType.F32):
+        st = Storage(0x50000000, nbytes)
+        return Tensor(st, dtype, list(shape), strides or row_major_strides(shape), offset)
+
+    # Row-major at a nonzero offset inside the storage passes every check.
+    assert encode_tensor_kind(tensor([5, 7], 4 * 38, offset=3)) == "UnsupportedDevice"
+    assert encode_tensor_kind(tensor([5, 7], 4 * 38, offset=4)) == "Shape"
+    # Not row-major: UnsupportedLayout, before the storage range.
+    assert encode_tensor_kind(tensor([5, 7], 4, strides=[1, 5])) == "UnsupportedLayout"
+    # Rank 9: the storage range (Shape) comes before encode_wire's rank check (Wire).
+    nine = [1] * 8 + [2]
+    assert encode_tensor_kind(tensor(nine, 4)) == "Shape"
+    assert encode_tensor_kind(tensor(nine, 8)) == "Wire"
+    # An extent above u32::MAX is the header's Shape once the range is in the storage.
+    assert encode_tensor_kind(tensor([1 << 32], 4 << 32)) == "Shape"
+    # An undecodable dtype tag is Wire before anything else.
+    assert encode_tensor_kind(tensor([5, 7], 4, strides=[1, 5], dtype=7), out_cap=200) == "Wire"
+    # An output buffer shorter than the message.
+    assert encode_tensor_kind(tensor([5, 7], 4 * 35), out_cap=16 + 8 + 139) == "Shape"
+    assert encode_tensor_kind(tensor([5, 7], 4 * 35), out_cap=16 + 8 + 140) == "UnsupportedDevice"

@@ -33,6 +33,20 @@ def test_tensor_to_wire_and_back_is_bit_exact(hb, dtype, shape):
     assert hb.download(fresh) == raw
 
 
+@pytest.mark.parametrize("dtype,offset,shape", [(B.DType.F32, 3, [5, 7]), (B.DType.BF16, 1, [33, 9]),
+                                                (B.DType.F16, 1000, [2, 1, 3]), (B.DType.F32, 41, [])])
+def test_tensor_at_an_offset_encodes_its_own_bytes(hb, dtype, offset, shape):
+    # download accepts row-major strides at any in-bounds offset (crates/cpu/src/lib.rs:183-194).
+    n = int(np.prod(shape)) if shape else 1
+    size = dtype.size_of()
+    total = offset + n + 5
+    raw = rng(offset).integers(0, 256, total * size, dtype=np.uint8).tobytes()
+    whole = hb.upload(dtype, [total], raw)
+    t = B.Tensor(whole.storage, dtype, list(shape), B.row_major_strides(shape), offset)
+    msg = W.encode_tensor(hb, t)
+    assert msg == W.encode(dtype, shape, raw[offset * size:(offset + n) * size])
+
+
 def test_boundary_activation_after_device_work(hb):
     # A boundary activation produced by the device: the message carries its final bytes.
     x = hb.upload_f32([256, 384], rng(2).standard_normal(256 * 384).astype(np.float32))
