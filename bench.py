@@ -132,6 +132,16 @@ def upload(pool, L, data: np.ndarray):
     return buf
 
 
+def kernels_of(ctx, call):
+    """Run `call` once and return the names of the kernels it launched (the launch log)."""
+    lib = native_lib()
+    before = lib.lg_debug_launch_count(ctx.handle)
+    call()
+    after = lib.lg_debug_launch_count(ctx.handle)
+    names = (lib.lg_debug_launch_name(ctx.handle, i) for i in range(max(before, after - 256), after))
+    return sorted(set(n.decode() for n in names if n))
+
+
 def bench_gemm(ctx, events, pool, L, C, name, m, n, k, args, a_t=False, b_t=False, batch=1,
                seed=(12, 13), sigma=None, beta=0.0):
     g = np.random.Generator(np.random.PCG64(seed[0]))
@@ -151,7 +161,8 @@ def bench_gemm(ctx, events, pool, L, C, name, m, n, k, args, a_t=False, b_t=Fals
           else L.TensorView.row_major(B, 0, bs + [k, n]))
     cv = L.TensorView.row_major(Cb, 0, bs + [m, n])
     plan = C.plan_gemm(1.0, av, bv, beta, cv)
-    C.encode_gemm(ctx, ctx.queue, 1.0, av, bv, beta, cv)  # validated once through Python
+    # Validated once through Python.
+    kernels = kernels_of(ctx, lambda: C.encode_gemm(ctx, ctx.queue, 1.0, av, bv, beta, cv))
     launch = abi_call(native_lib().lg_encode_gemm_f32, ctx.handle, ctx.queue.handle,
                       ctypes.c_float(1.0), av.to_c(), bv.to_c(), ctypes.c_float(beta), cv.to_c())
     ms = timed(ctx, events, launch, args.steps, args.warmup)
@@ -161,8 +172,9 @@ def bench_gemm(ctx, events, pool, L, C, name, m, n, k, args, a_t=False, b_t=Fals
     return {"name": name, "ms": ms, "ms_median": med, "ms_best": best,
             "host_ms": HOST_MS[launch], "tflops": tflops,
             "frac": tflops / PEAK_TFLOPS,
-            "plan": {k_: plan[k_] for k_ in ("kind", "a_mode", "b_mode", "splits", "workgroups")},
-            "_host": (a, b), "_geom": (m, n, k, a_t, b_t, batch, beta)}
+            "plan": {k_: plan[k_] for k_ in ("kind", "kernel", "tile", "a_mode", "b_mode",
+                                              "splits", "workgroups")},
+            "kernels": kernels, "_host": (a, b), "_geom": (m, n, k, a_t, b_t, batch, beta)}
 
 
 def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
@@ -173,7 +185,7 @@ def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
     src = P.permute_view(L.TensorView.row_major(src_buf, 0, shape), perm)
     dst = L.TensorView.row_major(dst_buf, 0, src.shape)
     plan = P.plan("materialize", src, dst)
-    P.encode_materialize(ctx, ctx.queue, src, dst)
+    kernels = kernels_of(ctx, lambda: P.encode_materialize(ctx, ctx.queue, src, dst))
     launch = abi_call(native_lib().lg_encode_materialize, ctx.handle, ctx.queue.handle, src.elem,
                       src.to_c(), dst.to_c())
     ms = timed(ctx, events, launch, args.steps, args.warmup)
@@ -182,7 +194,7 @@ def bench_perm(ctx, events, pool, L, P, name, shape, perm, seed, args):
     return {"name": name, "ms": ms, "ms_median": med, "ms_best": best,
             "host_ms": HOST_MS[launch], "gbs": gbs, "frac": gbs / PEAK_GBS,
             "plan": {k_: plan[k_] for k_ in ("kind", "vector", "workgroups", "shape")},
-            "_host": x, "_geom": (list(shape), list(perm))}
+            "kernels": kernels, "_host": x, "_geom": (list(shape), list(perm))}
 
 
 def bench_copy(ctx, events, pool, L, P, n, args):
@@ -219,7 +231,8 @@ def bench_contract(ctx, events, pool, L, C, name, a_spec, b_spec, c_spec, args, 
     flops = 2.0 * float(np.prod([float(e) for e in extents.values()]))
     nbytes = 4.0 * sum(float(np.prod(v.shape)) for v, _ in views)
     plan = C.plan_contract(1.0, views[0], views[1], 0.0, views[2])
-    C.encode_contract(ctx, ctx.queue, 1.0, views[0], views[1], 0.0, views[2])
+    kernels = kernels_of(ctx, lambda: C.encode_contract(ctx, ctx.queue, 1.0, views[0], views[1],
+                                                        0.0, views[2]))
     (av, la), (bv, lb), (cv, lc) = views
     launch = abi_call(native_lib().lg_encode_contract_f32, ctx.handle, ctx.queue.handle,
                       ctypes.c_float(1.0), av.to_c(), la.encode(), bv.to_c(), lb.encode(),
@@ -237,7 +250,7 @@ def bench_contract(ctx, events, pool, L, C, name, a_spec, b_spec, c_spec, args, 
             "tflops": tflops, "gbs": gbs, "flop": flops, "bytes": nbytes, "roofline": roof,
             "plan": {k_: plan[k_] for k_ in ("kind", "kernel", "tile", "a_mode", "b_mode",
                                               "splits", "workgroups", "swapped")},
-            "_other": (host, [(v.shape, v.strides, l) for v, l in views])}
+            "kernels": kernels, "_other": (host, [(v.shape, v.strides, l) for v, l in views])}
 
 
 def other_paths_specs():
@@ -705,8 +718,9 @@ def main() -> int:
                             "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                             "frac": round(head["frac"], 4),
                             "traffic": traffic_from_profile("gemm4096"),
-                            "kernel": "gemm_f32_mfma<0, 1, 16, 2, 2, false> (A K-contiguous, B N-contiguous, 128x128 tile)",
-                            "profile": "profiles/gemm_f32_mfma_gemm4096.md, profiles/traffic_gemm4096.txt",
+                            "kernel": ", ".join(head.get("kernels", [])) + " (A K-contiguous, B "
+                                      "N-contiguous, %dx%d tiles)" % tuple(head["plan"]["tile"]),
+                            "profile": "profiles/gemm_f32_dl_gemm4096.md, profiles/traffic_gemm4096.txt",
                             "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
     if head and "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
@@ -718,7 +732,7 @@ def main() -> int:
                                         "peak": PEAK_GBS, "unit": "GB/s",
                                         "frac": round(perm["frac"], 4),
                                         "traffic": traffic_from_profile("c2b"),
-                                        "kernel": "perm_tile<1, false, true, 128, 64, 3, 256> (non-temporal loads and stores)",
+                                        "kernel": ", ".join(perm.get("kernels", [])),
                                         "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
                                         "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
                            "cpu_baseline": perm.get("cpu_baseline"),
