@@ -9,7 +9,8 @@ benchmark configuration, each with its roofline fraction:
   contraction: achieved = 2*B*M*N*K / mean kernel time, peak = 157.3 TFLOP/s fp32 MFMA
   permutation: achieved = 2*numel*4 B / mean kernel time,  peak = 8000 GB/s HBM
 Kernel time is measured with HIP events recorded on the stream the kernels are launched on,
-around `steps` back-to-back launches after `warmup` untimed ones, with the stream synchronized
+around `steps` back-to-back launches after `warmup` untimed ones (and at least `--warmup-ms`
+of untimed launches, so short kernels reach the steady clock), with the stream synchronized
 on both sides. The CPU baseline times the C restatement of crates/cpu on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
@@ -68,15 +69,30 @@ class HipEvents:
 
 
 HOST_MS = {}  # host ms per enqueue call of the last timed() loop, by launch closure
+WARMUP_MS = 30.0  # least wall time of untimed launches per workload (--warmup-ms)
+
+
+def warm_up(ctx, launch, warmup):
+    """`warmup` untimed launches, then as many more as fill WARMUP_MS of wall time. The shader
+    clock settles over ~10-20 ms of a new load: 50 launches of a 90 us product (4.5 ms) time
+    config 4 at 90 us, 200 or more at 80-82 us, so short kernels get a time floor."""
+    t0 = time.perf_counter()
+    for _ in range(warmup):
+        launch()
+    ctx.sync()
+    spent = time.perf_counter() - t0
+    if WARMUP_MS > 0 and warmup > 0 and spent * 1e3 < WARMUP_MS:
+        per = spent / warmup
+        for _ in range(int((WARMUP_MS / 1e3 - spent) / max(per, 1e-6)) + 1):
+            launch()
+        ctx.sync()
 
 
 def timed(ctx, events, launch, steps, warmup):
     """Mean ms per launch over `steps` launches, bracketed by stream syncs. The host time of
     the enqueue loop is kept in HOST_MS: when it approaches the device time, the launches are
     bound by the caller's enqueue rate rather than by the kernels."""
-    for _ in range(warmup):
-        launch()
-    ctx.sync()
+    warm_up(ctx, launch, warmup)
     s = ctx.queue.handle
     e0, e1 = events.new(), events.new()
     events.record(e0, s)
@@ -579,6 +595,7 @@ def attach_cpu_baselines(results, threads):
 
 
 def main() -> int:
+    global WARMUP_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=20)
@@ -586,6 +603,10 @@ def main() -> int:
                     help="untimed launches before the timed ones; the MI355X needs tens of ms "
                          "of sustained MFMA load to reach its steady clock (5 launches of the "
                          "4096^3 GEMM measure ~7%% below steady state)")
+    ap.add_argument("--warmup-ms", type=float, default=WARMUP_MS,
+                    help="least wall time of untimed launches per workload after the --warmup "
+                         "ones (short kernels need more than 50 launches to reach the steady "
+                         "clock); 0 turns it off")
     ap.add_argument("--only", default=None,
                     help="run only these workloads (comma-separated): gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, "
                          "train, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, o_rank4, "
@@ -595,6 +616,7 @@ def main() -> int:
                     help="seconds of 4096^3 GEMMs to run before any timing, so workloads timed "
                          "alone start at the steady shader clock")
     args = ap.parse_args()
+    WARMUP_MS = args.warmup_ms
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
                           "n_gpus": args.gpus}))
@@ -708,6 +730,7 @@ def main() -> int:
     perm = results.get("c2b")
     line = {"metric": METRIC, "value": round(head["tflops"], 3) if head else None,
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "warmup_min_ms": args.warmup_ms,
             "ms_per_step": round(head["ms"], 4) if head else None, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
             "config": {"workload": "fp32 contraction C[4096,4096] = A.B row-major (north-star "
