@@ -142,27 +142,31 @@ __device__ inline void wait_slices(uint32_t newer) {
     wait_vm<0>();
 }
 
-// WM x WN waves, each 2x2 blocks of 32x32: a (64 WM) x (64 WN) tile of 64 WM WN threads
-// (2x2: 128x128; 2x4: 128x256, whose B slice serves twice the rows; 4x4: 256x256).
+// WM x WN waves, each FM x FN blocks of 32x32: a (32 FM WM) x (32 FN WN) tile of 64 WM WN
+// threads (2x2 waves of 2x2 blocks: 128x128; 2x4 waves: 128x256, whose B slice serves twice
+// the rows; 2x2 waves of 2x4 blocks: 128x256 with half the waves, each reading 6 fragments per
+// 8 MFMAs instead of 4 per 4).
 template <int WM, int WN>
 constexpr int dl_threads() { return 64 * WM * WN; }
-template <int NS, int BK, int WM, int WN>
+template <int NS, int BK, int WM, int WN, int FM, int FN>
 constexpr int dl_occupancy() {
-    // workgroups per compute unit by LDS (160 KB), at most what 128 VGPRs per wave allow
-    constexpr int lds = NS * (64 * WM + 64 * WN) * BK * 4;
+    // workgroups per compute unit by LDS (160 KB), at most what the accumulators allow: 2x2
+    // blocks (64 registers) fit four waves per SIMD, 2x4 two, 4x4 one
+    constexpr int lds = NS * (32 * FM * WM + 32 * FN * WN) * BK * 4;
     constexpr int by_lds = 160 * 1024 / lds;
-    constexpr int by_vgpr = 16 / (WM * WN);
+    constexpr int waves_per_simd = FM * FN <= 4 ? 4 : FM * FN <= 8 ? 2 : 1;
+    constexpr int by_vgpr = 4 * waves_per_simd / (WM * WN) > 0 ? 4 * waves_per_simd / (WM * WN) : 1;
     return by_lds < by_vgpr ? by_lds : by_vgpr;
 }
 
-template <int AM, int BMD, int NS, int BK = 16, int WN = 2, int WM = 2>
-__global__ __launch_bounds__((dl_threads<WM, WN>()), (dl_occupancy<NS, BK, WM, WN>()))
+template <int AM, int BMD, int NS, int BK = 16, int WN = 2, int WM = 2, int FM = 2, int FN = 2>
+__global__ __launch_bounds__((dl_threads<WM, WN>()), (dl_occupancy<NS, BK, WM, WN, FM, FN>()))
 void gemm_f32_dl(GemmArgs p) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
     static_assert(NS >= 2 && NS <= 4, "stages");
     static_assert(BK == 16 || BK == 32, "slice depth");
     constexpr int T = dl_threads<WM, WN>();
-    constexpr int RA = 64 * WM, RB = 64 * WN;
+    constexpr int RA = 32 * FM * WM, RB = 32 * FN * WN;
     using GA = DlGeo<RA, BK, T>;
     using GB = DlGeo<RB, BK, T>;
     constexpr int NW = T / 64;
@@ -189,11 +193,11 @@ void gemm_f32_dl(GemmArgs p) {
     const float alpha_a = p.scale_b ? 1.0f : p.alpha;
     const float alpha_b = p.scale_b ? p.alpha : 1.0f;
 
-    floatx16 acc[2][2];
+    floatx16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -249,18 +253,18 @@ void gemm_f32_dl(GemmArgs p) {
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int g = 0; g < BK / 8; ++g) {
-            floatx4 av[2], bv[2];
-            dl_frag<AM, RA, BK, 2>(av, as, wm * 64, g, lr, h);
-            dl_frag<BMD, RB, BK, 2>(bv, bs, wn * 64, g, lr, h);
+            floatx4 av[FM], bv[FN];
+            dl_frag<AM, RA, BK, FM>(av, as, wm * 32 * FM, g, lr, h);
+            dl_frag<BMD, RB, BK, FN>(bv, bs, wn * 32 * FN, g, lr, h);
             if (alpha_a != 1.0f) {
-                av[0] = av[0] * alpha_a;
-                av[1] = av[1] * alpha_a;
+#pragma unroll
+                for (int i = 0; i < FM; ++i) av[i] = av[i] * alpha_a;
             }
             if (alpha_b != 1.0f) {
-                bv[0] = bv[0] * alpha_b;
-                bv[1] = bv[1] * alpha_b;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) bv[j] = bv[j] * alpha_b;
             }
-            mfma_group<2, 2>(acc, av, bv);
+            mfma_group<FM, FN>(acc, av, bv);
         }
         __builtin_amdgcn_s_setprio(0);
     }
@@ -269,26 +273,26 @@ void gemm_f32_dl(GemmArgs p) {
     if (p.partial != nullptr) {
         float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                    const uint32_t col = n0 + wn * 64 + j * 32 + lr;
+                    const uint32_t row = m0 + wm * 32 * FM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                    const uint32_t col = n0 + wn * 32 * FN + j * 32 + lr;
                     if (inner || (row < p.m && col < p.n)) P[static_cast<int64_t>(row) * p.n + col] = acc[i][j][r];
                 }
         return;
     }
     float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                const uint32_t col = n0 + wn * 64 + j * 32 + lr;
+                const uint32_t row = m0 + wm * 32 * FM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                const uint32_t col = n0 + wn * 32 * FN + j * 32 + lr;
                 if (inner || (row < p.m && col < p.n)) {
                     float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
                     float v = acc[i][j][r];

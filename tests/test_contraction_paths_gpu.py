@@ -3,8 +3,8 @@
 * one 32x32 tile per wave (batches of small products),
 * sixteen waves per 32x32 tile with the K range split over workgroups (small outputs with
   long K), partials added in a fixed order,
-* dot products on the VALU (M = N = 1), split along K, the partials added in order by the
-  workgroup that draws the last ticket,
+* dot products on the VALU (M = N = 1), split along K, the partials added in order by a
+  second launch,
 * C stored contiguous along M, computed as C^T = B^T.A^T (alpha still scales A's elements),
 * K <= 8 on the VALU in the reference's own order, bit for bit against crates/cpu.
 
@@ -134,9 +134,9 @@ def test_dot_batched_offset_and_strided(ctx, pool):
         case.scalars(1.25, -0.5).run(ctx, pool, 300 + i)
 
 
-def test_dot_split_tickets_stay_consistent_across_calls(ctx, pool):
-    """The split dot's ticket words must be back at zero after every call: a run of calls of
-    different split counts and batches gives each one's own bits, also when repeated."""
+def test_dot_split_partials_stay_consistent_across_calls(ctx, pool):
+    """The split dot's partials share the context's buffer: a run of calls of different split
+    counts and batches gives each one's own bits, also when repeated."""
     shapes = [(1, 1 << 20), (3, 200000), (1, 70000), (2, 1 << 19)]
     outs = {}
     for rep in range(2):

@@ -108,8 +108,8 @@ def test_captured_gemm_and_transpose_replay_like_eager_work(ctx, pool):
 
 
 def test_captured_split_products_replay_like_eager_work(ctx, pool):
-    """Split-K (128x128 tiles), split 32x32 tiles and a split dot under capture: the partials and
-    tickets live in the context's scratch, so capture needs no allocation; three replays on new
+    """Split-K (128x128 tiles), split 32x32 tiles and a split dot under capture: the partials live
+    in the context's scratch, so capture needs no allocation; three replays on new
     inputs, eager runs of the same products between them, all bit for bit equal."""
     hip = Hip()
     q = ctx.new_stream()

@@ -1,10 +1,10 @@
 """lg_encode_gemm_f32_noalloc against lg_encode_gemm_f32, through the C ABI.
 
-The entry point allocates nothing: split-K partials and dot tickets live in a static device
+The entry point allocates nothing: split-K and split-dot partials live in a static device
 array. Its results must be the existing entry point's (the same plans, so bit for bit) and
 pass the north-star bound against the crates/cpu restatement, over calls in a row whose later
-inputs are smaller (the array keeps the last call's contents, so stale partials or tickets
-would show), on the context stream and on a caller's stream. An invalid call returns its
+inputs are smaller (the array keeps the last call's contents, so stale partials would
+show), on the context stream and on a caller's stream. An invalid call returns its
 status and launches nothing.
 """
 from __future__ import annotations
@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 SHAPES = [
     (256, 256, 65536),  # split-K, 128 splits: the full 32 MiB of partials
     (64, 48, 30000),    # 32x32 tiles of sixteen waves, split along K
-    (1, 1, 1 << 20),    # split dot: tickets
+    (1, 1, 1 << 20),    # split dot
     (1, 1, 100003),     # a smaller split dot
     (300, 200, 100),    # one tiled launch, no scratch
     (256, 128, 9000),   # split-K again, fewer and smaller partials
