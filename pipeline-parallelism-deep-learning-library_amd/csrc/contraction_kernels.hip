@@ -395,7 +395,9 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
 
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args) {
     const uint64_t count = static_cast<uint64_t>(args.m) * args.n * args.batch;
-    const int v = args.n % 4 == 0 ? 4 : 1;
+    // Small outputs take one output per lane, so more workgroups share the splits' loads
+    // (32x32 outputs: 16 workgroups instead of 4). The sum's order does not depend on V.
+    const int v = args.n % 4 == 0 && count >= 65536 ? 4 : 1;
     const uint64_t per = static_cast<uint64_t>(RED_LANES) * v;
     const uint64_t g = (count + per - 1) / per;
     const dim3 grid(static_cast<uint32_t>(g < 65536 ? (g ? g : 1) : 65536));

@@ -271,8 +271,8 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_contract(1.0, (dense([32, 1 << 20]), "mk"), (t(1 << 20, 32), "kn"), 0.0,
                         (dense([32, 32]), "mn"))
     assert (p["kind"], p["kernel"], p["tile"]) == ("split", "small", (32, 32))
-    assert (p["a_mode"], p["b_mode"]) == ("k", "k") and p["workgroups"] == p["splits"] == 512
-    assert p["scratch_bytes"] == 512 * 32 * 32 * 4 <= 32 << 20
+    assert (p["a_mode"], p["b_mode"]) == ("k", "k") and p["workgroups"] == p["splits"] == 256
+    assert p["k_chunk"] == 4096 and p["scratch_bytes"] == 256 * 32 * 32 * 4 <= 32 << 20
     # "rank-1 4096^2" and "rank-4 ijkl,klmn->ijmn 48^6" (axes merge to a 2304^3 product).
     # K <= 8 runs on the VALU in crates/cpu's own order, four outputs per thread.
     p = C.plan_contract(1.0, (dense([4096, 1]), "mk"), (dense([1, 4096]), "kn"), 0.0,
