@@ -608,7 +608,7 @@ def main() -> int:
                          "ones (short kernels need more than 50 launches to reach the steady "
                          "clock); 0 turns it off")
     ap.add_argument("--only", default=None,
-                    help="run only these workloads (comma-separated): gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, "
+                    help="run only these workloads (comma-separated): gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, floor, "
                          "train, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, o_rank4, "
                          "o_f16_2048")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -709,6 +709,22 @@ def main() -> int:
                                "source": "tests/permutation_test.rs:741-792"}
         return r
     run("t8191", t8191)
+
+    def floor():
+        # The launch floor of the small-product paths: C[32,32] = 0 (K = 0, one fill kernel)
+        # through the same entry point, back to back and one at a time between events.
+        a, b, c = pool.alloc("f32", 1), pool.alloc("f32", 1), pool.alloc("f32", 32 * 32)
+        av = L.TensorView(a, 0, [32, 0], [1, 1])
+        bv = L.TensorView(b, 0, [0, 32], [32, 1])
+        cv = L.TensorView.row_major(c, 0, [32, 32])
+        kernels = kernels_of(ctx, lambda: C.encode_gemm(ctx, ctx.queue, 1.0, av, bv, 0.0, cv))
+        launch = abi_call(native_lib().lg_encode_gemm_f32, ctx.handle, ctx.queue.handle,
+                          ctypes.c_float(1.0), av.to_c(), bv.to_c(), ctypes.c_float(0.0), cv.to_c())
+        ms = timed(ctx, events, launch, args.steps, args.warmup)
+        med, best = per_launch(ctx, events, launch, args.steps)
+        return {"name": "launch floor: C[32,32] = 0 (K = 0)", "ms": ms, "ms_median": med,
+                "ms_best": best, "host_ms": HOST_MS[launch], "kernels": kernels}
+    run("floor", floor)
     run("train", lambda: bench_train_ops(events, args, timed))
     run("f16", lambda: bench_gemm_f16(ctx, events, pool, L, C, 4096, 4096, 4096, args))
     # The reference's own benchmark list (tests/contraction_test.rs:1293-1395).
