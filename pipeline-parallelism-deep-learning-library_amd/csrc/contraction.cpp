@@ -539,6 +539,28 @@ void small_split_shape(uint64_t tiles, uint32_t k, uint64_t split_bytes, uint32_
     *splits = static_cast<uint32_t>((k + c - 1) / c);
 }
 
+// The same for small outputs split along long K onto one-wave 32x32 direct-load tiles:
+// SKINNY_SPLIT_TARGET workgroups in all (about four per compute unit, each with three 8 KB
+// stages of loads in flight), each chunk at least SKINNY_MIN_CHUNK and a multiple of the
+// 32-deep slice (32x32 with K = 2^20: 512 workgroups 68 us, 1024 51 us, 2048 51 us).
+constexpr uint32_t SKINNY_SPLIT_TARGET = 1024;
+constexpr uint32_t SKINNY_MIN_CHUNK = 256;
+constexpr uint32_t SKINNY_BK = 32;
+void skinny_split_shape(uint64_t tiles, uint32_t k, uint64_t split_bytes, uint32_t* splits,
+                        uint32_t* chunk) {
+    *splits = 1;
+    *chunk = k;
+    if (tiles >= SKINNY_SPLIT_TARGET || k < 2 * SKINNY_MIN_CHUNK) return;
+    const uint64_t want = (SKINNY_SPLIT_TARGET + tiles - 1) / tiles;
+    const uint64_t rough = std::max<uint64_t>(
+        1, std::min<uint64_t>({want, k / SKINNY_MIN_CHUNK, SPLIT_MAX, SPLIT_PARTIAL_MAX / split_bytes}));
+    uint64_t c = (k + rough - 1) / rough;
+    c = (c + SKINNY_BK - 1) / SKINNY_BK * SKINNY_BK;
+    if (c >= k) return;
+    *chunk = static_cast<uint32_t>(c);
+    *splits = static_cast<uint32_t>((k + c - 1) / c);
+}
+
 // The dot path's split: DOT_TARGET workgroups in all, each chunk at least DOT_MIN_CHUNK and a
 // multiple of 1024 (four elements for each of 256 threads).
 void dot_split_shape(uint32_t batch, uint32_t k, uint32_t* splits, uint32_t* chunk) {
@@ -797,18 +819,34 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     t.tiles_n = (nn + t.tile_n - 1) / t.tile_n;
     info.tile_m = t.tile;
     info.tile_n = t.tile_n;
-    info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
-                  : t.kernel == KERN_DIRECT ? LG_KERNEL_DIRECT
-                  : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
-                                            : LG_KERNEL_WAVE;
     const uint64_t tiles = static_cast<uint64_t>(t.tiles_m) * t.tiles_n * batch;
     const uint64_t split_bytes = static_cast<uint64_t>(batch) * mm * nn * sizeof(float);
     uint32_t splits = 1, chunk = k;
     if (t.kernel == KERN_TILE || t.kernel == KERN_DIRECT) {
         split_shape(tiles, k, split_bytes, &splits, &chunk);
     } else if (t.kernel == KERN_SMALL && !(mid < GEMM_SMALL_BELOW && k <= GEMM_SMALL_K)) {
-        small_split_shape(tiles, k, split_bytes, &splits, &chunk);
+        // Small outputs with long K. Whole 32x32 tiles whose operands both have a 16-byte
+        // aligned unit-stride axis go to one-wave direct-load tiles when the split fills the
+        // chip: their loads read 8 rows x 128 B per wave instruction, where the sixteen-wave
+        // kernel's go straight to MFMA registers at 32 rows x 32 B (32x32 with K = 2^20: 68 ->
+        // 51 us). Other outputs keep the sixteen-wave kernel.
+        uint32_t ds = 1, dc = k;
+        const bool whole = mm % GEMM_TINY_TILE == 0 && nn % GEMM_TINY_TILE == 0;
+        if (whole && a_mode != LOAD_S && b_mode != LOAD_S) {
+            skinny_split_shape(tiles, k, split_bytes, &ds, &dc);
+        }
+        if (ds > 1 && tiles * ds >= GEMM_CUS) {
+            t.kernel = KERN_DIRECT;
+            splits = ds;
+            chunk = dc;
+        } else {
+            small_split_shape(tiles, k, split_bytes, &splits, &chunk);
+        }
     }
+    info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
+                  : t.kernel == KERN_DIRECT ? LG_KERNEL_DIRECT
+                  : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
+                                            : LG_KERNEL_WAVE;
     if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
     t.splits = splits;
     t.k_chunk = chunk;

@@ -1,18 +1,19 @@
 // The fp32 MFMA GEMM with operand slices copied from HBM straight into LDS.
 //
-// gemm_f32_dl<AM, BMD, NS>: the 128x128-tile product of gemm_f32_mfma (256 threads, four waves
-// in 2x2, each 2x2 blocks of v_mfma_f32_32x32x2_f32), with K-slices of 16 moved by
+// gemm_f32_dl<AM, BMD, NS, BK, WN, WM, FM, FN>: WM x WN waves, each FM x FN blocks of
+// v_mfma_f32_32x32x2_f32, over a (32 FM WM) x (32 FN WN) output tile (128x128, 128x256, and
+// 32x32 with one wave for small outputs split along long K), with K-slices of BK moved by
 // global_load_lds_dwordx4: each lane's 16 bytes land in LDS without passing through VGPRs, so
 // no staging registers, no LDS write instructions and no wait on the loads before the writes.
-// NS unpadded LDS stages (8 KB per operand each) keep NS - 1 slices in flight; one barrier per
-// slice. A wave instruction fills 1 KB of LDS contiguously (lane l at byte 16*l), so the layout
-// is chosen by which global chunk each lane fetches:
-//   LOAD_K  (unit stride along K): [row][k], 64 B per row; 16-byte chunk c of row r at chunk
-//            position c ^ swz_k(r) of the row, so the 32 rows an MFMA fragment read touches
-//            fall on distinct banks (for 8- and for 16-lane LDS phases);
-//   LOAD_MN (unit stride along M/N): [k][row], 512 B per k; chunk c (rows 4c..4c+3) of k-row kr
-//            at position c ^ swz_mn(kr), so the two lane halves (k and k + 4) of a 32-bit
-//            fragment read fall on different banks.
+// NS unpadded LDS stages keep NS - 1 slices in flight; one barrier per slice. A wave
+// instruction fills 1 KB of LDS contiguously (lane l at byte 16*l), so the layout is chosen by
+// which global chunk each lane fetches:
+//   LOAD_K  (unit stride along K): [row][k], 4*BK bytes per row; 16-byte chunk c of row r at
+//            chunk position c ^ swz_k(r) of the row, so the 32 rows an MFMA fragment read
+//            touches fall on distinct banks (for 8- and for 16-lane LDS phases);
+//   LOAD_MN (unit stride along M/N): [k][row], 4*R bytes per k; chunk c (rows 4c..4c+3) of
+//            k-row kr at position c ^ swz_mn(kr), so the two lane halves (k and k + 4) of a
+//            32-bit fragment read fall on different banks.
 // Edge tiles and a partial last K-slice are loaded through registers into the same layout
 // (elements outside the operand as zero). alpha scales the fragments of the operand holding
 // the caller's A as they are read, so every product is (alpha*a)*b.
@@ -39,7 +40,8 @@ struct DlGeo {
 // Chunk swizzles. [row][k] with BK = 16 (four chunks a row): rows r, r+2, r+4, r+6 and r, r+4,
 // r+8, r+12 get distinct chunk positions; with BK = 32 (eight chunks): any eight consecutive
 // rows, and the rows of one parity among sixteen. [k][row]: k-rows four apart differ by eight
-// chunks (128 bytes).
+// chunks (128 bytes) when a k-row holds at least 16 chunks (R >= 64); a 32-row k-row (128
+// bytes, every bank once) is left as it is.
 template <int BK>
 __device__ inline uint32_t swz_k(uint32_t r) {
     if constexpr (BK == 16) {
@@ -48,7 +50,11 @@ __device__ inline uint32_t swz_k(uint32_t r) {
         return (r ^ (r >> 3)) & 7u;
     }
 }
-__device__ inline uint32_t swz_mn(uint32_t kr) { return ((kr >> 2) & 1u) * 8u; }
+template <int R>
+__device__ inline uint32_t swz_mn(uint32_t kr) {
+    static_assert(R == 32 || R % 64 == 0, "k-row width");
+    return R >= 64 ? ((kr >> 2) & 1u) * 8u : 0u;
+}
 
 // Chunk position q of a stage -> (operand row, k) of its first element, relative to the
 // tile's (row 0, k of the slice).
@@ -61,7 +67,7 @@ __device__ inline void dl_chunk(uint32_t q, uint32_t* row, uint32_t* k) {
     } else {
         constexpr uint32_t CPK = R / 4;   // chunks per k-row
         *k = q / CPK;
-        *row = 4 * ((q % CPK) ^ swz_mn(q / CPK));
+        *row = 4 * ((q % CPK) ^ swz_mn<R>(q / CPK));
     }
 }
 
@@ -71,7 +77,7 @@ __device__ inline uint32_t dl_at(uint32_t row, uint32_t k) {
     if constexpr (MODE == LOAD_K) {
         return row * BK + 4 * ((k >> 2) ^ swz_k<BK>(row)) + (k & 3u);
     } else {
-        return k * R + 4 * ((row >> 2) ^ swz_mn(k)) + (row & 3u);
+        return k * R + 4 * ((row >> 2) ^ swz_mn<R>(k)) + (row & 3u);
     }
 }
 

@@ -267,12 +267,20 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     assert (p["kind"], p["kernel"], p["a_mode"]) == ("dot", "dot", "k")
     assert p["splits"] * p["k_chunk"] >= 1 << 24 and p["k_chunk"] % 1024 == 0
     assert p["workgroups"] == p["splits"] == 2048 and p["scratch_bytes"] == 4 * 2048
-    # "32x32 K=1M" (B column-major): sixteen waves per 32x32 tile, split along K.
+    # "32x32 K=1M" (B column-major): one-wave 32x32 direct-load tiles, split along K.
     p = C.plan_contract(1.0, (dense([32, 1 << 20]), "mk"), (t(1 << 20, 32), "kn"), 0.0,
                         (dense([32, 32]), "mn"))
-    assert (p["kind"], p["kernel"], p["tile"]) == ("split", "small", (32, 32))
-    assert (p["a_mode"], p["b_mode"]) == ("k", "k") and p["workgroups"] == p["splits"] == 256
-    assert p["k_chunk"] == 4096 and p["scratch_bytes"] == 256 * 32 * 32 * 4 <= 32 << 20
+    assert (p["kind"], p["kernel"], p["tile"]) == ("split", "direct", (32, 32))
+    assert (p["a_mode"], p["b_mode"]) == ("k", "k") and p["workgroups"] == p["splits"] == 1024
+    assert p["k_chunk"] == 1024 and p["scratch_bytes"] == 1024 * 32 * 32 * 4 <= 32 << 20
+    # The same output with A strided along K (no aligned unit-stride axis) or a ragged 30x32
+    # output keeps the sixteen-wave kernel.
+    p = C.plan_contract(1.0, (view(Layout(0, [32, 1 << 19], [1 << 20, 2])), "mk"),
+                        (t(1 << 19, 32), "kn"), 0.0, (dense([32, 32]), "mn"))
+    assert (p["kind"], p["kernel"], p["a_mode"]) == ("split", "small", "strided")
+    p = C.plan_contract(1.0, (dense([30, 1 << 20]), "mk"), (t(1 << 20, 32), "kn"), 0.0,
+                        (dense([30, 32]), "mn"))
+    assert (p["kind"], p["kernel"], p["workgroups"]) == ("split", "small", 256)
     # "rank-1 4096^2" and "rank-4 ijkl,klmn->ijmn 48^6" (axes merge to a 2304^3 product).
     # K <= 8 runs on the VALU in crates/cpu's own order, four outputs per thread.
     p = C.plan_contract(1.0, (dense([4096, 1]), "mk"), (dense([1, 4096]), "kn"), 0.0,

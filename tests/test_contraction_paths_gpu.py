@@ -103,6 +103,64 @@ def test_small_split_is_bitwise_deterministic_and_transposed_c(ctx, pool):
 
 
 # --------------------------------------------------------------------------------------
+# one-wave 32x32 direct-load tiles, split along long K
+# --------------------------------------------------------------------------------------
+def _matrix(rows, cols, cm):
+    return Layout.transposed(rows, cols) if cm else dense([rows, cols])
+
+
+@pytest.mark.parametrize("a_cm,b_cm,c_cm", [(False, True, False), (False, False, False),
+                                            (True, False, False), (True, True, True),
+                                            (False, False, True)])
+def test_skinny_direct_load_tiles(ctx, pool, a_cm, b_cm, c_cm):
+    """Three whole 32x32 tiles with K = 70012: 244 splits of 288 (the last 28 deep, through the
+    register path), every pair of operand layouts (K- or M/N-contiguous, so both [row][k] and
+    the 32-row [k][row] stage layouts), C row- or column-major (the swapped roles). Checked
+    against the exact f64 product under the north-star bound and against the reference's gate,
+    and bitwise equal over two runs."""
+    m, n, k = 32, 96, 70012
+    alpha, beta = 1.25, -0.5
+    g = rng(700 + 4 * a_cm + 2 * b_cm + c_cm)
+    x = g.uniform(-1, 1, m * k).astype(np.float32)
+    y = g.uniform(-1, 1, k * n).astype(np.float32)
+    c0 = g.uniform(-1, 1, m * n).astype(np.float32)
+    la, lb, lc = _matrix(m, k, a_cm), _matrix(k, n, b_cm), _matrix(m, n, c_cm)
+    a, b = Tensor(pool, la, x), Tensor(pool, lb, y)
+    p = C.plan_gemm(alpha, a.view(), b.view(), beta, Tensor(pool, lc).view())
+    assert (p["kind"], p["kernel"], p["tile"], p["splits"], p["k_chunk"]) == \
+        ("split", "direct", (32, 32), 244, 288), p
+    assert p["swapped"] == c_cm
+    outs = []
+    for _ in range(2):
+        c = Tensor(pool, lc, c0)
+        C.gemm(ctx, alpha, a.view(), b.view(), beta, c.view())
+        outs.append(c.read()[: m * n].copy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    # Logical matrices from the stored words.
+    A = (x.reshape(k, m).T if a_cm else x.reshape(m, k)).astype(np.float64)
+    B = (y.reshape(n, k).T if b_cm else y.reshape(k, n)).astype(np.float64)
+    C0 = (c0.reshape(n, m).T if c_cm else c0.reshape(m, n)).astype(np.float64)
+    got = outs[0].reshape(n, m).T if c_cm else outs[0].reshape(m, n)
+    exact = alpha * (A @ B) + beta * C0
+    _gate_north_star("skinny direct vs exact", got.ravel(), exact.ravel(), k, alpha, 1.0)
+    e = oracle.contract_f64(alpha, x, (0, la.shape, la.strides), "mk", y, (0, lb.shape, lb.strides),
+                            "kn", beta, c0.copy(), (0, lc.shape, lc.strides), "mn")
+    oracle.gate(outs[0], e, "skinny direct")
+
+
+def test_skinny_direct_load_batched_with_permuted_b(ctx, pool):
+    """Three batches of 32x32 with K = 40000 and B a permuted view ("bnk" storage read as
+    bkn): 139 splits per batch, 417 workgroups."""
+    bsz, m, n, k = 3, 32, 32, 40000
+    case = Case("skinny batched", (dense([bsz, m, k]), "bmk"),
+                (Layout.with_([bsz, k, n], [0, 2, 1], [1, 1, 1], 0), "bkn"),
+                (dense([bsz, m, n]), "bmn")).scalars(0.5, 0.0)
+    p = plan_of(case, pool)
+    assert (p["kind"], p["kernel"], p["tile"], p["splits"]) == ("split", "direct", (32, 32), 139), p
+    case.run(ctx, pool, 4242)
+
+
+# --------------------------------------------------------------------------------------
 # dot products
 # --------------------------------------------------------------------------------------
 @pytest.mark.parametrize("k", [1, 3, 4, 1000, 1023, 8192, 8195, 100000, 262147])
