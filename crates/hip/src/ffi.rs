@@ -84,6 +84,8 @@ pub struct lg_contract_plan {
     pub tile_n: u32,
     pub kernel: u32,
     pub swapped: u32,
+    pub kgroups: u32,
+    pub reserved: u32,
 }
 
 #[repr(C)]

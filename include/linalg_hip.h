@@ -423,6 +423,10 @@ typedef struct lg_contract_plan {
                              products, 1x4 for K <= 8; f16: 64x64 */
     uint32_t kernel;      /* lg_plan_kernel */
     uint32_t swapped;     /* 1 when C is contiguous along M and is computed as C^T = B^T.A^T */
+    uint32_t kgroups;     /* LG_KERNEL_DIRECT: wave groups per workgroup splitting the tile's K
+                             slices (2 when the grid leaves at most one workgroup per compute
+                             unit), else 1 */
+    uint32_t reserved;
 } lg_contract_plan;
 
 lg_status lg_plan_contract_f32(float alpha, const lg_view* a, const char* a_labels,

@@ -579,6 +579,8 @@ void dot_split_shape(uint32_t batch, uint32_t k, uint32_t* splits, uint32_t* chu
 
 // Compute units of one MI355X, for the tile-size choice only.
 constexpr uint64_t GEMM_CUS = 256;
+// K elements per chunk below which two wave groups would each get too few slices to pipeline.
+constexpr uint32_t KG_MIN_CHUNK = 256;
 
 // Waves a many-tile 32x32 product needs before it takes one tile per wave (gemm_f32_wave)
 // rather than sixteen waves per tile (gemm_f32_small).
@@ -848,6 +850,14 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
                   : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
                                             : LG_KERNEL_WAVE;
     if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
+    // 128x128 direct-load grids that leave at most one workgroup per compute unit (four waves,
+    // one per SIMD) run two wave groups per workgroup on the two halves of each K chunk, so
+    // every SIMD has a second wave to issue MFMAs while the first waits.
+    t.kgroups = t.kernel == KERN_DIRECT && t.tile == GEMM_BM && t.tile_n == GEMM_BN &&
+                        tiles * splits <= GEMM_CUS && chunk >= KG_MIN_CHUNK
+                    ? 2
+                    : 1;
+    info.kgroups = t.kgroups;
     t.splits = splits;
     t.k_chunk = chunk;
     info.splits = splits;

@@ -15,7 +15,11 @@
 //            k-row kr at position c ^ swz_mn(kr), so the two lane halves (k and k + 4) of a
 //            32-bit fragment read fall on different banks.
 // Edge tiles and a partial last K-slice are loaded through registers into the same layout
-// (elements outside the operand as zero). alpha scales the fragments of the operand holding
+// (elements outside the operand as zero). With KG = 2 the workgroup holds two such wave groups,
+// each with its own stages, taking the first and the second half of the tile's K slices; the
+// second group's sums are added to the first's through LDS at the end (group 0 + group 1,
+// the same order every run), which gives a grid of one workgroup per compute unit two waves
+// per SIMD. alpha scales the fragments of the operand holding
 // the caller's A as they are read, so every product is (alpha*a)*b.
 #pragma once
 
@@ -154,36 +158,44 @@ __device__ inline void wait_slices(uint32_t newer) {
 // 8 MFMAs instead of 4 per 4).
 template <int WM, int WN>
 constexpr int dl_threads() { return 64 * WM * WN; }
-template <int NS, int BK, int WM, int WN, int FM, int FN>
+template <int NS, int BK, int WM, int WN, int FM, int FN, int KG = 1>
 constexpr int dl_occupancy() {
     // workgroups per compute unit by LDS (160 KB), at most what the accumulators allow: 2x2
     // blocks (64 registers) fit four waves per SIMD, 2x4 two, 4x4 one
-    constexpr int lds = NS * (32 * FM * WM + 32 * FN * WN) * BK * 4;
+    constexpr int lds = KG * NS * (32 * FM * WM + 32 * FN * WN) * BK * 4;
     constexpr int by_lds = 160 * 1024 / lds;
     constexpr int waves_per_simd = FM * FN <= 4 ? 4 : FM * FN <= 8 ? 2 : 1;
-    constexpr int by_vgpr = 4 * waves_per_simd / (WM * WN) > 0 ? 4 * waves_per_simd / (WM * WN) : 1;
+    constexpr int waves = WM * WN * KG;
+    constexpr int by_vgpr = 4 * waves_per_simd / waves > 0 ? 4 * waves_per_simd / waves : 1;
     return by_lds < by_vgpr ? by_lds : by_vgpr;
 }
 
-template <int AM, int BMD, int NS, int BK = 16, int WN = 2, int WM = 2, int FM = 2, int FN = 2>
-__global__ __launch_bounds__((dl_threads<WM, WN>()), (dl_occupancy<NS, BK, WM, WN, FM, FN>()))
+template <int AM, int BMD, int NS, int BK = 16, int WN = 2, int WM = 2, int FM = 2, int FN = 2,
+          int KG = 1>
+__global__ __launch_bounds__((dl_threads<WM, WN>() * KG), (dl_occupancy<NS, BK, WM, WN, FM, FN, KG>()))
 void gemm_f32_dl(GemmArgs p) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
     static_assert(NS >= 2 && NS <= 4, "stages");
     static_assert(BK == 16 || BK == 32, "slice depth");
-    constexpr int T = dl_threads<WM, WN>();
+    static_assert(KG == 1 || KG == 2, "wave groups");
+    constexpr int T = dl_threads<WM, WN>();  // threads of one wave group
     constexpr int RA = 32 * FM * WM, RB = 32 * FN * WN;
     using GA = DlGeo<RA, BK, T>;
     using GB = DlGeo<RB, BK, T>;
     constexpr int NW = T / 64;
-    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
-    float* As = smem;
-    float* Bs = smem + NS * GA::ST;
+    constexpr int GROUP_ST = NS * (GA::ST + GB::ST);  // floats of one group's stages
+    constexpr int RED = NW * FM * FN * 16 * 64;      // floats of one group's accumulators
+    static_assert(KG == 1 || RED <= KG * GROUP_ST, "the group sums must fit in the stages");
+    __shared__ __attribute__((aligned(16))) float smem[KG * GROUP_ST];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int kg = (tid >> 6) / NW;    // wave group
+    const int wave = (tid >> 6) % NW;  // wave within its group
     const int wm = wave / WN, wn = wave % WN;
     const int lr = lane & 31, h = lane >> 5;
+    float* As = smem + kg * GROUP_ST;
+    float* Bs = As + NS * GA::ST;
 
     uint32_t plane, tm, tn;
     decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
@@ -210,6 +222,11 @@ void gemm_f32_dl(GemmArgs p) {
     const bool inner = mrem >= RA && nrem >= RB;
     const uint32_t ktiles = (klen + BK - 1) / BK;
     const uint32_t kfull = inner ? klen / BK : 0;  // slices that go by direct loads
+    // Group kg takes slices [kg * per, kg * per + mine); every group runs `per` iterations so
+    // all waves meet at the same barriers.
+    const uint32_t per = (ktiles + KG - 1) / KG;
+    const uint32_t first = min(static_cast<uint32_t>(kg) * per, ktiles);
+    const uint32_t mine = min(per, ktiles - first);
     // Per-thread source offsets of the direct loads at k = 0, and the k step per slice.
     int64_t sa[GA::LOADS], sb[GB::LOADS];
 #pragma unroll
@@ -219,9 +236,11 @@ void gemm_f32_dl(GemmArgs p) {
     const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
     const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
 
-    auto issue = [&](uint32_t kt) {
-        float* as = As + (kt % NS) * GA::ST;
-        float* bs = Bs + (kt % NS) * GB::ST;
+    // Slice i of this group (global slice first + i) into stage i % NS.
+    auto issue = [&](uint32_t i) {
+        float* as = As + (i % NS) * GA::ST;
+        float* bs = Bs + (i % NS) * GB::ST;
+        const uint32_t kt = first + i;
         if (kt < kfull) {
 #pragma unroll
             for (int i = 0; i < GA::LOADS; ++i) dl_copy16(A + sa[i] + kt * a_step, as + (i * NW + wave) * 256);
@@ -246,14 +265,16 @@ void gemm_f32_dl(GemmArgs p) {
 
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) {
-        if (static_cast<uint32_t>(s) < ktiles) issue(s);
+        if (static_cast<uint32_t>(s) < mine) issue(s);
     }
-    for (uint32_t kt = 0; kt < ktiles; ++kt) {
-        const uint32_t ahead = min(static_cast<uint32_t>(NS - 2), ktiles - 1 - kt);
-        wait_slices<NS, GA::LOADS + GB::LOADS>(ahead);
+    for (uint32_t kt = 0; kt < per; ++kt) {
+        // Group-uniform: a group with fewer slices still meets every barrier.
+        const bool live = kt < mine;
+        if (live) wait_slices<NS, GA::LOADS + GB::LOADS>(min(static_cast<uint32_t>(NS - 2), mine - 1 - kt));
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
-        if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
+        if (!live) continue;
+        if (kt + NS - 1 < mine) issue(kt + NS - 1);
         const float* as = As + (kt % NS) * GA::ST;
         const float* bs = Bs + (kt % NS) * GB::ST;
         __builtin_amdgcn_s_setprio(1);
@@ -273,6 +294,29 @@ void gemm_f32_dl(GemmArgs p) {
             mfma_group<FM, FN>(acc, av, bv);
         }
         __builtin_amdgcn_s_setprio(0);
+    }
+
+    if constexpr (KG == 2) {
+        // Group 1's sums to LDS (every stage read and every load landed: each group waited for
+        // its last slice before the final barrier), then group 0 adds them in and stores.
+        __syncthreads();
+        float* red = smem + (wave * FM * FN * 16) * 64 + lane;
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + red[((i * FN + j) * 16 + r) * 64];
     }
 
     // Epilogue: as gemm_f32_mfma.

@@ -168,6 +168,9 @@ struct GemmArgs {
     // KERN_OUTER: 1 when C is contiguous along N, n % 4 == 0 and every row 16-byte aligned
     // (128-bit stores), and (vec_b) the same for B (128-bit loads).
     uint32_t vec_c, vec_b;
+    // KERN_DIRECT: wave groups per workgroup that take the tile's K slices in halves and add
+    // their sums in group order at the end (1 or 2).
+    uint32_t kgroups;
 };
 
 // Dot products (M = N = 1): C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k]. Split along K

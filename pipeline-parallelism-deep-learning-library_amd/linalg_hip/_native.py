@@ -39,7 +39,8 @@ class lg_contract_plan(ctypes.Structure):
     _fields_ = [("kind", u32), ("a_mode", u32), ("b_mode", u32), ("groups", u32),
                 ("batch", u64), ("m", u64), ("n", u64), ("k", u64), ("splits", u64),
                 ("k_chunk", u64), ("workgroups", u64), ("scratch_bytes", u64), ("tile_m", u32),
-                ("tile_n", u32), ("kernel", u32), ("swapped", u32)]
+                ("tile_n", u32), ("kernel", u32), ("swapped", u32), ("kgroups", u32),
+                ("reserved", u32)]
 
 
 class lg_permute_plan(ctypes.Structure):

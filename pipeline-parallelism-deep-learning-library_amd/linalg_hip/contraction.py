@@ -85,7 +85,7 @@ def _plan_dict(p: N.lg_contract_plan) -> dict:
             "n": p.n, "k": p.k, "splits": p.splits, "k_chunk": p.k_chunk,
             "workgroups": p.workgroups, "scratch_bytes": p.scratch_bytes,
             "tile": (p.tile_m, p.tile_n), "kernel": N.PLAN_KERNELS[p.kernel],
-            "swapped": bool(p.swapped)}
+            "swapped": bool(p.swapped), "kgroups": int(p.kgroups)}
 
 
 def plan_contract(alpha: float, a, b, beta: float, c) -> dict:

@@ -775,3 +775,33 @@ def test_wide_direct_load_batched_with_permuted_b(ctx, pool):
                          ref, 0, (n, 1))
         err = np.abs(got[bi * m * n:(bi + 1) * m * n].astype(np.float64) - ref.astype(np.float64))
         assert float(err.max()) <= 1e-5 * np.sqrt(k) * 0.5 + 1e-5, (bi, float(err.max()))
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2048, 2048, 2048, False, False, False),
+                                            (1952, 2040, 1004, True, False, False),
+                                            (2040, 1932, 300, False, True, True),
+                                            (2048, 1924, 260, True, True, False)])
+def test_two_wave_groups_per_workgroup(ctx, pool, m, n, k, ta, tb, tc):
+    """Grids of exactly 256 128x128 direct-load tiles (one workgroup per compute unit) run two
+    wave groups per workgroup, each on half of the K slices, their sums added in group order:
+    ragged M and N edges, odd slice counts (the second group one slice short: K = 1004, 63
+    slices; K = 260, 17), partial last slices (K = 1004, 300, 260), every operand layout, and C
+    column-major, against crates/cpu on every element; the same bits over two runs."""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(7500 + m + n + k)
+    alpha, beta = (1.0, 0.0) if not (ta or tb) else (0.75, -0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"]) == \
+        ("direct", (128, 128), 2, 256), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"two groups {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
