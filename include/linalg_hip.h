@@ -424,8 +424,8 @@ typedef struct lg_contract_plan {
     uint32_t kernel;      /* lg_plan_kernel */
     uint32_t swapped;     /* 1 when C is contiguous along M and is computed as C^T = B^T.A^T */
     uint32_t kgroups;     /* LG_KERNEL_DIRECT: wave groups per workgroup splitting the tile's K
-                             slices (2 when the grid leaves at most one workgroup per compute
-                             unit), else 1 */
+                             slices when the grid leaves at most one workgroup per compute unit
+                             (2 for 128x128 tiles, 4 for 64x64), else 1 */
     uint32_t reserved;
 } lg_contract_plan;
 

@@ -581,6 +581,8 @@ void dot_split_shape(uint32_t batch, uint32_t k, uint32_t* splits, uint32_t* chu
 constexpr uint64_t GEMM_CUS = 256;
 // K elements per chunk below which two wave groups would each get too few slices to pipeline.
 constexpr uint32_t KG_MIN_CHUNK = 256;
+// Longest K for which 64x64 tiles replace a split 128x128 grid.
+constexpr uint32_t FILLS64_MAX_K = 4096;
 
 // Waves a many-tile 32x32 product needs before it takes one tile per wave (gemm_f32_wave)
 // rather than sixteen waves per tile (gemm_f32_small).
@@ -792,7 +794,15 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
         const uint64_t rounds_big = (big + GEMM_CUS - 1) / GEMM_CUS;
         const uint64_t rounds_mid = (mid + GEMM_CUS - 1) / GEMM_CUS;
         const bool uneven = big >= GEMM_CUS && 20 * rounds_mid < 68 * rounds_big;
-        t.tile = big * k_ways < GEMM_SMALL_BELOW || uneven ? GEMM_SMALL_TILE : GEMM_BM;
+        // A 128x128 grid that would need split-K to fill the chip takes 64x64 tiles when those
+        // alone fill it in (nearly) whole rounds and K is short, so the split chunks would be
+        // only a few slices deep (1024^3: 64 tiles split 8 ways, 54 TFLOP/s; 256 64x64 tiles,
+        // 73; 1024x2048x1024: 75 -> 89). Otherwise the split grid balances better (1280^3, 400
+        // 64x64 tiles: 71 against 80; 1536^3: 79 against 87; 1536^2 x 65536: 83 against 110).
+        const uint64_t rounds64 = (mid + GEMM_CUS - 1) / GEMM_CUS;
+        const bool fills64 = big < GEMM_CUS && mid >= GEMM_CUS && 10 * mid >= 9 * rounds64 * GEMM_CUS &&
+                             k <= FILLS64_MAX_K;
+        t.tile = big * k_ways < GEMM_SMALL_BELOW || uneven || fills64 ? GEMM_SMALL_TILE : GEMM_BM;
         t.kernel = KERN_TILE;
     } else if (2 * useful >= mid * GEMM_SMALL_TILE * GEMM_SMALL_TILE) {
         t.tile = GEMM_SMALL_TILE;
@@ -845,19 +855,28 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             small_split_shape(tiles, k, split_bytes, &splits, &chunk);
         }
     }
+    if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
+    // Grids that leave at most one workgroup per compute unit (four waves, one per SIMD) run
+    // several wave groups per workgroup on consecutive parts of each K chunk, so every SIMD has
+    // more waves to issue MFMAs while one waits: 128x128 direct-load tiles two groups (2048^3:
+    // 107 -> 117 TFLOP/s), 64x64 tiles with aligned operands four groups of 32-deep slices on
+    // the direct-load kernel (1024^3: 68 -> 77).
+    t.kgroups = 1;
+    if (tiles * splits <= GEMM_CUS) {
+        if (t.kernel == KERN_DIRECT && t.tile == GEMM_BM && t.tile_n == GEMM_BN &&
+            chunk >= KG_MIN_CHUNK) {
+            t.kgroups = 2;
+        } else if (t.kernel == KERN_TILE && t.tile == GEMM_SMALL_TILE && a_mode != LOAD_S &&
+                   b_mode != LOAD_S && chunk >= 2 * KG_MIN_CHUNK) {
+            t.kernel = KERN_DIRECT;
+            t.kgroups = 4;
+        }
+    }
+    info.kgroups = t.kgroups;
     info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
                   : t.kernel == KERN_DIRECT ? LG_KERNEL_DIRECT
                   : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
                                             : LG_KERNEL_WAVE;
-    if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
-    // 128x128 direct-load grids that leave at most one workgroup per compute unit (four waves,
-    // one per SIMD) run two wave groups per workgroup on the two halves of each K chunk, so
-    // every SIMD has a second wave to issue MFMAs while the first waits.
-    t.kgroups = t.kernel == KERN_DIRECT && t.tile == GEMM_BM && t.tile_n == GEMM_BN &&
-                        tiles * splits <= GEMM_CUS && chunk >= KG_MIN_CHUNK
-                    ? 2
-                    : 1;
-    info.kgroups = t.kgroups;
     t.splits = splits;
     t.k_chunk = chunk;
     info.splits = splits;

@@ -323,6 +323,9 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         if constexpr (AM != LOAD_S && BMD != LOAD_S) {
             if (a.tile == GEMM_TINY_TILE) {
                 hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 3, 32, 1, 1, 1, 1>), dim3(groups), dim3(64), 0, s, a);
+            } else if (a.tile == GEMM_SMALL_TILE) {
+                if (a.kgroups != 4) fail_invalid("64x64 direct-load tiles run four wave groups");
+                hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 2, 32, 2, 2, 1, 1, 4>), dim3(groups), dim3(1024), 0, s, a);
             } else if (a.kgroups == 2) {
                 hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 3, 16, 2, 2, 2, 2, 2>), dim3(groups), dim3(512), 0, s, a);
             } else if (a.tile_n == GEMM_WIDE_N) {

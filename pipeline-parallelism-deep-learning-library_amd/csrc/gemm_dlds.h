@@ -15,11 +15,10 @@
 //            k-row kr at position c ^ swz_mn(kr), so the two lane halves (k and k + 4) of a
 //            32-bit fragment read fall on different banks.
 // Edge tiles and a partial last K-slice are loaded through registers into the same layout
-// (elements outside the operand as zero). With KG = 2 the workgroup holds two such wave groups,
-// each with its own stages, taking the first and the second half of the tile's K slices; the
-// second group's sums are added to the first's through LDS at the end (group 0 + group 1,
-// the same order every run), which gives a grid of one workgroup per compute unit two waves
-// per SIMD. alpha scales the fragments of the operand holding
+// (elements outside the operand as zero). With KG = 2 or 4 the workgroup holds that many such
+// wave groups, each with its own stages, taking consecutive parts of the tile's K slices; the
+// other groups' sums are added to group 0's through LDS at the end (in group order, the same
+// every run), which gives a grid of one workgroup per compute unit more waves per SIMD. alpha scales the fragments of the operand holding
 // the caller's A as they are read, so every product is (alpha*a)*b.
 #pragma once
 
@@ -177,7 +176,7 @@ void gemm_f32_dl(GemmArgs p) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
     static_assert(NS >= 2 && NS <= 4, "stages");
     static_assert(BK == 16 || BK == 32, "slice depth");
-    static_assert(KG == 1 || KG == 2, "wave groups");
+    static_assert(KG == 1 || KG == 2 || KG == 4, "wave groups");
     constexpr int T = dl_threads<WM, WN>();  // threads of one wave group
     constexpr int RA = 32 * FM * WM, RB = 32 * FN * WN;
     using GA = DlGeo<RA, BK, T>;
@@ -185,7 +184,7 @@ void gemm_f32_dl(GemmArgs p) {
     constexpr int NW = T / 64;
     constexpr int GROUP_ST = NS * (GA::ST + GB::ST);  // floats of one group's stages
     constexpr int RED = NW * FM * FN * 16 * 64;      // floats of one group's accumulators
-    static_assert(KG == 1 || RED <= KG * GROUP_ST, "the group sums must fit in the stages");
+    static_assert((KG - 1) * RED <= KG * GROUP_ST, "the group sums must fit in the stages");
     __shared__ __attribute__((aligned(16))) float smem[KG * GROUP_ST];
 
     const int tid = threadIdx.x;
@@ -296,27 +295,31 @@ void gemm_f32_dl(GemmArgs p) {
         __builtin_amdgcn_s_setprio(0);
     }
 
-    if constexpr (KG == 2) {
-        // Group 1's sums to LDS (every stage read and every load landed: each group waited for
-        // its last slice before the final barrier), then group 0 adds them in and stores.
+    if constexpr (KG > 1) {
+        // The other groups' sums to LDS (every stage read and every load landed: each group
+        // waited for its last slice before the final barrier), then group 0 adds them in group
+        // order and stores.
         __syncthreads();
         float* red = smem + (wave * FM * FN * 16) * 64 + lane;
-        if (kg == 1) {
+        if (kg > 0) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) red[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+                    for (int r = 0; r < 16; ++r) red[(kg - 1) * RED + ((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
         }
         __syncthreads();
-        if (kg == 1) return;
+        if (kg > 0) return;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int g = 1; g < KG; ++g)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + red[((i * FN + j) * 16 + r) * 64];
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[i][j][r] = acc[i][j][r] + red[(g - 1) * RED + ((i * FN + j) * 16 + r) * 64];
     }
 
     // Epilogue: as gemm_f32_mfma.

@@ -298,9 +298,24 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     assert (p["kind"], p["splits"], p["workgroups"]) == ("dot", 1, 4096)
     p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 16]), 0.0, dense([4096, 16]))
     assert p["tile"] == (32, 32) and p["kernel"] == "small" and p["kind"] == "split"
-    # The split count is capped so the partials fit the context's 32 MiB scratch.
-    p = C.plan_gemm(1.0, dense([1536, 65536]), dense([65536, 1536]), 0.0, dense([1536, 1536]))
-    assert p["kind"] == "split" and p["scratch_bytes"] <= 32 << 20
+    # The split count is capped so the partials fit the context's 32 MiB scratch: 384^2 wants
+    # 57 splits of 576 KiB, 56 fit.
+    p = C.plan_gemm(1.0, dense([384, 65536]), dense([65536, 384]), 0.0, dense([384, 384]))
+    assert (p["kind"], p["splits"]) == ("split", 56) and p["scratch_bytes"] <= 32 << 20
+    # 128x128 grids that would need split-K take 64x64 tiles when those fill the chip; one
+    # workgroup per compute unit runs four wave groups on the direct-load kernel (1024^3), or
+    # two on 128x128 tiles (2048^3).
+    p = C.plan_gemm(1.0, dense([1024, 1024]), dense([1024, 2048]), 0.0, dense([1024, 2048]))
+    assert (p["kind"], p["tile"], p["workgroups"]) == ("tiled", (64, 64), 512)
+    for m, n, k in [(1536, 1536, 1536), (1280, 1280, 1280), (1024, 1024, 8192)]:
+        p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
+        assert (p["kind"], p["tile"]) == ("split", (128, 128)), (m, n, k, p)
+    p = C.plan_gemm(1.0, dense([1024, 1024]), dense([1024, 1024]), 0.0, dense([1024, 1024]))
+    assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (64, 64), 4)
+    p = C.plan_gemm(1.0, dense([2048, 2048]), dense([2048, 2048]), 0.0, dense([2048, 2048]))
+    assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (128, 128), 2)
+    p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 4096]), 0.0, dense([4096, 4096]))
+    assert (p["tile"], p["kgroups"]) == ((128, 256), 1)
 
 
 def test_contraction_plans_for_the_baseline_configs():

@@ -805,3 +805,33 @@ def test_two_wave_groups_per_workgroup(ctx, pool, m, n, k, ta, tb, tc):
     assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
     _gemm_fast_check(f"two groups {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(1024, 1024, 1024, False, False, False),
+                                            (1000, 1020, 900, True, False, False),
+                                            (1020, 968, 1000, False, True, True),
+                                            (964, 1024, 516, True, True, False)])
+def test_four_wave_groups_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
+    """Grids of exactly 256 64x64 tiles (a 128x128 grid would need split-K) on the direct-load
+    kernel with four wave groups of 32-deep slices: ragged edges, groups with fewer slices
+    than the others (K = 900: 8, 8, 8, 5 slices; K = 516: 5, 5, 5, 2), partial last slices,
+    every operand layout and C column-major, against crates/cpu on every element; the same
+    bits over two runs."""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(7600 + m + n + k)
+    alpha, beta = (1.0, 0.0) if not (ta or tb) else (-1.25, 0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"]) == \
+        ("direct", (64, 64), 4, 256), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"four groups {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
