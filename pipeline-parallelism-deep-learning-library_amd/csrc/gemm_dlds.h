@@ -184,7 +184,7 @@ void gemm_f32_dl(GemmArgs p) {
     constexpr int NW = T / 64;
     constexpr int GROUP_ST = NS * (GA::ST + GB::ST);  // floats of one group's stages
     constexpr int RED = NW * FM * FN * 16 * 64;      // floats of one group's accumulators
-    static_assert((KG - 1) * RED <= KG * GROUP_ST, "the group sums must fit in the stages");
+    static_assert((KG / 2) * RED <= KG * GROUP_ST, "the group sums must fit in the stages");
     __shared__ __attribute__((aligned(16))) float smem[KG * GROUP_ST];
 
     const int tid = threadIdx.x;
@@ -296,30 +296,35 @@ void gemm_f32_dl(GemmArgs p) {
     }
 
     if constexpr (KG > 1) {
-        // The other groups' sums to LDS (every stage read and every load landed: each group
-        // waited for its last slice before the final barrier), then group 0 adds them in group
-        // order and stores.
-        __syncthreads();
+        // The groups' sums meet through LDS in a fixed tree (every stage read and every load
+        // landed: each group waited for its last slice before the final barrier): with four
+        // groups (g0 + g2) + (g1 + g3), with two g0 + g1. Every wave takes part in every
+        // barrier; group 0 stores.
         float* red = smem + (wave * FM * FN * 16) * 64 + lane;
-        if (kg > 0) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+        for (int step = KG / 2; step >= 1; step /= 2) {
+            __syncthreads();
+            if (kg >= step && kg < 2 * step) {
 #pragma unroll
-                for (int j = 0; j < FN; ++j)
+                for (int i = 0; i < FM; ++i)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) red[(kg - 1) * RED + ((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            red[(kg - step) * RED + ((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+            }
+            __syncthreads();
+            if (kg < step) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            acc[i][j][r] = acc[i][j][r] + red[kg * RED + ((i * FN + j) * 16 + r) * 64];
+            }
         }
-        __syncthreads();
         if (kg > 0) return;
-#pragma unroll
-        for (int g = 1; g < KG; ++g)
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        acc[i][j][r] = acc[i][j][r] + red[(g - 1) * RED + ((i * FN + j) * 16 + r) * 64];
     }
 
     // Epilogue: as gemm_f32_mfma.
