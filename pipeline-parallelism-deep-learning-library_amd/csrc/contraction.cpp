@@ -858,9 +858,10 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     if (tiles * splits > 0x7fffffffull) fail_invalid("problem exceeds one launch's workgroup count");
     // Grids that leave at most one workgroup per compute unit (four waves, one per SIMD) run
     // several wave groups per workgroup on consecutive parts of each K chunk, so every SIMD has
-    // more waves to issue MFMAs while one waits: 128x128 direct-load tiles two groups (2048^3:
-    // 107 -> 117 TFLOP/s), 64x64 tiles with aligned operands four groups of 32-deep slices on
-    // the direct-load kernel (1024^3: 68 -> 77).
+    // more waves to issue MFMAs while one waits: 128x128 direct-load tiles two groups of
+    // 32-deep slices in two stages (2048^3: 107 -> 119 TFLOP/s; three groups 117, four 112),
+    // 64x64 tiles with aligned operands four groups of 32-deep slices on the direct-load
+    // kernel (1024^3: 68 -> 77).
     t.kgroups = 1;
     if (tiles * splits <= GEMM_CUS) {
         if (t.kernel == KERN_DIRECT && t.tile == GEMM_BM && t.tile_n == GEMM_BN &&

@@ -327,7 +327,7 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
                 if (a.kgroups != 4) fail_invalid("64x64 direct-load tiles run four wave groups");
                 hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 2, 32, 2, 2, 1, 1, 4>), dim3(groups), dim3(1024), 0, s, a);
             } else if (a.kgroups == 2) {
-                hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 3, 16, 2, 2, 2, 2, 2>), dim3(groups), dim3(512), 0, s, a);
+                hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 2, 32, 2, 2, 2, 2, 2>), dim3(groups), dim3(512), 0, s, a);
             } else if (a.tile_n == GEMM_WIDE_N) {
                 hipLaunchKernelGGL((gemm_f32_dl<AM, BMD, 3, 16, 4>), dim3(groups), dim3(512), 0, s, a);
             } else {

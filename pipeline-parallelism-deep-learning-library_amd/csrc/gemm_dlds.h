@@ -42,15 +42,18 @@ struct DlGeo {
 
 // Chunk swizzles. [row][k] with BK = 16 (four chunks a row): rows r, r+2, r+4, r+6 and r, r+4,
 // r+8, r+12 get distinct chunk positions; with BK = 32 (eight chunks): any eight consecutive
-// rows, and the rows of one parity among sixteen. [k][row]: k-rows four apart differ by eight
+// rows, and the rows of one parity among sixteen; with BK = 64 (sixteen chunks): any sixteen
+// consecutive rows. [k][row]: k-rows four apart differ by eight
 // chunks (128 bytes) when a k-row holds at least 16 chunks (R >= 64); a 32-row k-row (128
 // bytes, every bank once) is left as it is.
 template <int BK>
 __device__ inline uint32_t swz_k(uint32_t r) {
     if constexpr (BK == 16) {
         return ((r >> 1) ^ (r >> 3)) & 3u;
-    } else {
+    } else if constexpr (BK == 32) {
         return (r ^ (r >> 3)) & 7u;
+    } else {
+        return (r ^ (r >> 4)) & 15u;
     }
 }
 template <int R>
@@ -175,8 +178,8 @@ __global__ __launch_bounds__((dl_threads<WM, WN>() * KG), (dl_occupancy<NS, BK, 
 void gemm_f32_dl(GemmArgs p) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
     static_assert(NS >= 2 && NS <= 4, "stages");
-    static_assert(BK == 16 || BK == 32, "slice depth");
-    static_assert(KG == 1 || KG == 2 || KG == 4, "wave groups");
+    static_assert(BK == 16 || BK == 32 || BK == 64, "slice depth");
+    static_assert(KG >= 1 && KG <= 4, "wave groups");
     constexpr int T = dl_threads<WM, WN>();  // threads of one wave group
     constexpr int RA = 32 * FM * WM, RB = 32 * FN * WN;
     using GA = DlGeo<RA, BK, T>;
@@ -189,8 +192,10 @@ void gemm_f32_dl(GemmArgs p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int kg = (tid >> 6) / NW;    // wave group
-    const int wave = (tid >> 6) % NW;  // wave within its group
+    // Wave group and wave within it; with one group these are compile-time 0 and the wave id,
+    // so the single-group kernel keeps its straight loop.
+    const int kg = KG == 1 ? 0 : (tid >> 6) / NW;
+    const int wave = KG == 1 ? (tid >> 6) : (tid >> 6) % NW;
     const int wm = wave / WN, wn = wave % WN;
     const int lr = lane & 31, h = lane >> 5;
     float* As = smem + kg * GROUP_ST;
@@ -223,9 +228,9 @@ void gemm_f32_dl(GemmArgs p) {
     const uint32_t kfull = inner ? klen / BK : 0;  // slices that go by direct loads
     // Group kg takes slices [kg * per, kg * per + mine); every group runs `per` iterations so
     // all waves meet at the same barriers.
-    const uint32_t per = (ktiles + KG - 1) / KG;
-    const uint32_t first = min(static_cast<uint32_t>(kg) * per, ktiles);
-    const uint32_t mine = min(per, ktiles - first);
+    const uint32_t per = KG == 1 ? ktiles : (ktiles + KG - 1) / KG;
+    const uint32_t first = KG == 1 ? 0u : min(static_cast<uint32_t>(kg) * per, ktiles);
+    const uint32_t mine = KG == 1 ? ktiles : min(per, ktiles - first);
     // Per-thread source offsets of the direct loads at k = 0, and the k step per slice.
     int64_t sa[GA::LOADS], sb[GB::LOADS];
 #pragma unroll
@@ -268,7 +273,7 @@ void gemm_f32_dl(GemmArgs p) {
     }
     for (uint32_t kt = 0; kt < per; ++kt) {
         // Group-uniform: a group with fewer slices still meets every barrier.
-        const bool live = kt < mine;
+        const bool live = KG == 1 || kt < mine;
         if (live) wait_slices<NS, GA::LOADS + GB::LOADS>(min(static_cast<uint32_t>(NS - 2), mine - 1 - kt));
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
@@ -297,24 +302,26 @@ void gemm_f32_dl(GemmArgs p) {
 
     if constexpr (KG > 1) {
         // The groups' sums meet through LDS in a fixed tree (every stage read and every load
-        // landed: each group waited for its last slice before the final barrier): with four
-        // groups (g0 + g2) + (g1 + g3), with two g0 + g1. Every wave takes part in every
-        // barrier; group 0 stores.
+        // landed: each group waited for its last slice before the final barrier): each round
+        // the upper half of the groups still holding sums hands them to the lower half, so
+        // four groups add as (g0 + g2) + (g1 + g3), three as (g0 + g2) + g1, two as g0 + g1.
+        // Every wave takes part in every barrier; group 0 stores.
         float* red = smem + (wave * FM * FN * 16) * 64 + lane;
 #pragma unroll
-        for (int step = KG / 2; step >= 1; step /= 2) {
+        for (int n = KG; n > 1; n = (n + 1) / 2) {
+            const int half = (n + 1) / 2;
             __syncthreads();
-            if (kg >= step && kg < 2 * step) {
+            if (kg >= half && kg < n) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            red[(kg - step) * RED + ((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+                            red[(kg - half) * RED + ((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
             }
             __syncthreads();
-            if (kg < step) {
+            if (kg < n - half) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
