@@ -522,7 +522,8 @@ def traffic_from_profile(name):
 
 # Bounded CPU samples per GEMM workload: (literal rows, rows for the threaded variant or None
 # for all, batches for the threaded variant). About 20 s of CPU work for the whole set.
-CPU_GEMM_SAMPLES = {"gemm4096": (48, None, 1), "c1": (512, None, 1), "c3": (32, None, 4),
+CPU_GEMM_SAMPLES = {"gemm4096": (48, None, 1), "sq1024": (256, None, 1), "sq2048": (64, None, 1),
+                    "c1": (512, None, 1), "c3": (32, None, 4),
                     "c4": (4, None, 1), "c5": (4, 256, 1)}
 
 
@@ -550,6 +551,51 @@ def repeat_for(fn, min_s=0.25):
         dt = time.perf_counter() - t0
         if dt >= min_s:
             return runs, dt
+
+
+VENDOR_SHAPES = {"gemm4096": (1, 4096, 4096, 4096, False), "sq1024": (1, 1024, 1024, 1024, False),
+                 "sq2048": (1, 2048, 2048, 2048, False), "c3": (32, 1024, 1024, 1024, True)}
+
+
+def attach_vendor(results, args):
+    """The vendor library on the same shapes (the reference times MPSMatrixMultiplication beside
+    its own kernel): torch.matmul in fp32 with TF32 off, which runs hipBLASLt, timed with torch's
+    events on torch's stream after the same warm-up. `ratio` = this library's TFLOP/s over
+    the vendor's."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda", 0)
+    for name, (batch, m, n, k, b_t) in VENDOR_SHAPES.items():
+        r = results.get(name)
+        if not isinstance(r, dict) or "tflops" not in r:
+            continue
+        g = torch.Generator(device=dev).manual_seed(7)
+        a = torch.rand((batch, m, k), device=dev, generator=g) * 2 - 1
+        b = torch.rand((batch, n, k) if b_t else (batch, k, n), device=dev, generator=g) * 2 - 1
+        # Config 3's B is a permuted view for this library; the vendor gets it contiguous.
+        bb = b.transpose(1, 2).contiguous() if b_t else b
+        c = torch.empty((batch, m, n), device=dev)
+        step = (lambda: torch.matmul(a[0], bb[0], out=c[0])) if batch == 1 else \
+            (lambda: torch.matmul(a, bb, out=c))
+        t0 = time.perf_counter()
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        while time.perf_counter() - t0 < WARMUP_MS / 1e3:
+            step()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        tf = 2.0 * batch * m * n * k / (ms * 1e-3) / 1e12
+        r["vendor"] = {"tflops": tf, "ms": ms, "ratio": r["tflops"] / tf,
+                       "library": "hipBLASLt through torch.matmul, fp32, TF32 off" +
+                                  (", B contiguous" if b_t else "")}
+        del a, b, c
 
 
 def cpu_gemm_rates(host, geom, seq_rows, fast_rows, fast_batches, threads):
@@ -666,10 +712,14 @@ def main() -> int:
                          "ones (short kernels need more than 50 launches to reach the steady "
                          "clock); 0 turns it off")
     ap.add_argument("--only", default=None,
-                    help="run only these workloads (comma-separated): gemm4096, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, floor, "
+                    help="run only these workloads (comma-separated): gemm4096, sq1024, sq2048, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, floor, "
                          "train, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, o_rank4, "
                          "o_f16_2048")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time the vendor library on the square GEMMs and config 3, as the "
+                         "reference's spec benchmark does against MPS: torch.matmul in fp32 with "
+                         "TF32 off (hipBLASLt); imports torch")
     ap.add_argument("--prewarm", type=float, default=0.0,
                     help="seconds of 4096^3 GEMMs to run before any timing, so workloads timed "
                          "alone start at the steady shader clock")
@@ -725,6 +775,11 @@ def main() -> int:
             pool.free()
 
     run("gemm4096", lambda: bench_gemm(ctx, events, pool, L, C, "gemm 4096^3", 4096, 4096, 4096, args))
+    # The reference's spec benchmark squares (tests/contraction_test.rs:1246-1291).
+    run("sq1024", lambda: bench_gemm(ctx, events, pool, L, C, "square gemm 1024^3", 1024, 1024, 1024,
+                                     args, seed=(1024, 1025)))
+    run("sq2048", lambda: bench_gemm(ctx, events, pool, L, C, "square gemm 2048^3", 2048, 2048, 2048,
+                                     args, seed=(2048, 2049)))
     run("c1", lambda: bench_gemm(ctx, events, pool, L, C, "C1 gemm 512^3", 512, 512, 512, args, seed=(1, 2)))
     run("c3", lambda: bench_gemm(ctx, events, pool, L, C, "C3 bik,bkj->bij B=32 1024^3, B permuted",
                                  1024, 1024, 1024, args, b_t=True, batch=32, seed=(5, 6)))
@@ -791,6 +846,9 @@ def main() -> int:
         run(key, lambda: bench_contract(ctx, events, pool, L, C, name, a_spec, b_spec, c_spec, args))
     run("o_f16_2048", lambda: bench_gemm_f16(ctx, events, pool, L, C, 2048, 2048, 2048, args))
 
+    if args.vendor:
+        print("[bench] vendor ...", file=sys.stderr, flush=True)
+        attach_vendor(results, args)
     train = results.pop("train", None)
     if not args.no_cpu:
         print("[bench] cpu baselines ...", file=sys.stderr, flush=True)
