@@ -395,7 +395,8 @@ typedef enum lg_plan_kernel {
     LG_KERNEL_WAVE = 3,  /* one 32x32 tile per wave (batches of small products) */
     LG_KERNEL_DOT = 4,   /* one dot product (chunk) per workgroup */
     LG_KERNEL_OUTER = 5, /* K <= 8: four outputs per thread on the VALU, summed in k order */
-    LG_KERNEL_DIRECT = 6 /* 128x128 or 128x256 tile, operand slices loaded straight into LDS */
+    LG_KERNEL_DIRECT = 6, /* 128x128 or 128x256 tile, operand slices loaded straight into LDS */
+    LG_KERNEL_PIPELINED = 7 /* full 128x128 tiles, direct loads, software-pipelined waves */
 } lg_plan_kernel;
 
 /* Operand load modes of the tiled kernel. */
@@ -415,9 +416,11 @@ typedef struct lg_contract_plan {
     uint64_t k_chunk;     /* K elements per split */
     uint64_t workgroups;  /* workgroups of the main launch */
     uint64_t scratch_bytes; /* device scratch of the split-K partials */
-    uint32_t tile_m;      /* output tile of one workgroup or wave (tiled/split): 128x256 for */
-    uint32_t tile_n;      /* grids of at least 512 such tiles, else 128x128; 64x64 when 128x128
-                             tiles would leave most compute units idle or be mostly padding;
+    uint32_t tile_m;      /* output tile of one workgroup or wave (tiled/split): 128x128 on */
+    uint32_t tile_n;      /* the pipelined kernel (full tiles, at least 512 workgroups), else
+                             128x256 for grids of at least 512 such tiles, else 128x128; 64x64
+                             when 128x128 tiles would leave most compute units idle or be
+                             mostly padding;
                              32x32 for small outputs (sixteen waves per tile splitting K) and
                              batches of small products (one tile per wave); 1x1 for dot
                              products, 1x4 for K <= 8; f16: 64x64 */

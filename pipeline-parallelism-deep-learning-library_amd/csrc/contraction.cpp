@@ -873,8 +873,22 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             t.kgroups = 4;
         }
     }
+    // Full 128x128 tiles, K chunks in whole pipeline steps and at least two workgroups per
+    // compute unit: the software-pipelined kernel, 128x128 tiles also where 128x256 ones were
+    // chosen (4096^3: 137 -> 142 TFLOP/s; config 3 134 -> 138; config 4 106 -> 111; config
+    // 5 137.5 -> 142).
+    const uint32_t last_chunk = k - (splits - 1) * chunk;
+    if (t.kernel == KERN_DIRECT && t.kgroups == 1 && t.tile == GEMM_BM && mm % GEMM_BM == 0 &&
+        nn % GEMM_BN == 0 && chunk % PIPE_K_STEP == 0 && last_chunk % PIPE_K_STEP == 0 &&
+        static_cast<uint64_t>(mm / GEMM_BM) * (nn / GEMM_BN) * batch * splits >= 2 * GEMM_CUS) {
+        t.kernel = KERN_PIPE;
+        t.tile_n = GEMM_BN;
+        t.tiles_n = nn / GEMM_BN;
+        info.tile_n = GEMM_BN;
+    }
     info.kgroups = t.kgroups;
     info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
+                  : t.kernel == KERN_PIPE   ? LG_KERNEL_PIPELINED
                   : t.kernel == KERN_DIRECT ? LG_KERNEL_DIRECT
                   : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
                                             : LG_KERNEL_WAVE;

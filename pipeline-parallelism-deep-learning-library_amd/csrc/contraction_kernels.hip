@@ -9,6 +9,7 @@
 #include <algorithm>
 
 #include "gemm_dlds.h"
+#include "gemm_pipe.h"
 #include "gemm_kernel.h"
 #include "lg_internal.h"
 
@@ -17,6 +18,7 @@ namespace {
 
 using gemm_detail::gemm_f32_dl;
 using gemm_detail::gemm_f32_mfma;
+using gemm_detail::gemm_f32_pl;
 using gemm_detail::gemm_f32_small;
 using gemm_detail::gemm_f32_wave;
 using gemm_detail::SMALL_WAVES;
@@ -319,6 +321,22 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         } else {
             hipLaunchKernelGGL((outer_f32<false, false>), dim3(groups), dim3(OUTER_THREADS), 0, s, a);
         }
+    } else if (a.kernel == KERN_PIPE) {
+        if constexpr (AM != LOAD_S && BMD != LOAD_S) {
+            const uint32_t last = a.k - (a.splits - 1) * a.k_chunk;
+            if (a.tile != GEMM_BM || a.tile_n != GEMM_BN || a.m % GEMM_BM != 0 || a.n % GEMM_BN != 0 ||
+                a.k_chunk % PIPE_K_STEP != 0 || last % PIPE_K_STEP != 0) {
+                fail_invalid("the pipelined GEMM needs full 128x128 tiles and K chunks in whole steps");
+            }
+            if (AM == LOAD_K && BMD == LOAD_K && a.k_chunk >= PIPE_DEEP_K &&
+                a.k_chunk % PIPE_DEEP_STEP == 0 && last % PIPE_DEEP_STEP == 0) {
+                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 32, 4>), dim3(groups), dim3(256), 0, s, a);
+            } else {
+                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 16, 4>), dim3(groups), dim3(256), 0, s, a);
+            }
+        } else {
+            fail_invalid("the pipelined GEMM needs a unit-stride axis in both operands");
+        }
     } else if (a.kernel == KERN_DIRECT) {
         if constexpr (AM != LOAD_S && BMD != LOAD_S) {
             if (a.tile == GEMM_TINY_TILE) {
@@ -365,7 +383,7 @@ uint64_t gemm_workgroups(const GemmArgs& a) {
 
 void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, int b_mode) {
     const uint32_t groups = static_cast<uint32_t>(gemm_workgroups(args));
-    static const char* const names[5][3][3] = {
+    static const char* const names[6][3][3] = {
         {{"gemm_f32_mfma<K,K>", "gemm_f32_mfma<K,MN>", "gemm_f32_mfma<K,S>"},
          {"gemm_f32_mfma<MN,K>", "gemm_f32_mfma<MN,MN>", "gemm_f32_mfma<MN,S>"},
          {"gemm_f32_mfma<S,K>", "gemm_f32_mfma<S,MN>", "gemm_f32_mfma<S,S>"}},
@@ -380,8 +398,17 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
          {"gemm_f32_outer", "gemm_f32_outer", "gemm_f32_outer"}},
         {{"gemm_f32_dl<K,K>", "gemm_f32_dl<K,MN>", "gemm_f32_dl<K,S>"},
          {"gemm_f32_dl<MN,K>", "gemm_f32_dl<MN,MN>", "gemm_f32_dl<MN,S>"},
-         {"gemm_f32_dl<S,K>", "gemm_f32_dl<S,MN>", "gemm_f32_dl<S,S>"}}};
-    if (args.kernel > KERN_DIRECT) fail_invalid("unknown GEMM kernel");
+         {"gemm_f32_dl<S,K>", "gemm_f32_dl<S,MN>", "gemm_f32_dl<S,S>"}},
+        {{"gemm_f32_pl<K,K>", "gemm_f32_pl<K,MN>", "gemm_f32_pl<K,S>"},
+         {"gemm_f32_pl<MN,K>", "gemm_f32_pl<MN,MN>", "gemm_f32_pl<MN,S>"},
+         {"gemm_f32_pl<S,K>", "gemm_f32_pl<S,MN>", "gemm_f32_pl<S,S>"}}};
+    if (args.kernel > KERN_PIPE) fail_invalid("unknown GEMM kernel");
+    const char* name = names[args.kernel][a_mode][b_mode];
+    if (args.kernel == KERN_PIPE && a_mode == LOAD_K && b_mode == LOAD_K &&
+        args.k_chunk >= PIPE_DEEP_K && args.k_chunk % PIPE_DEEP_STEP == 0 &&
+        (args.k - (args.splits - 1) * args.k_chunk) % PIPE_DEEP_STEP == 0) {
+        name = "gemm_f32_pl32<K,K>";
+    }
 #define LG_GEMM_CASE(AMV, BMV)                       \
     if (a_mode == AMV && b_mode == BMV) {            \
         launch_gemm_t<AMV, BMV>(s, args, groups);    \
@@ -397,7 +424,7 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
     LG_GEMM_CASE(LOAD_S, LOAD_S) { fail_invalid("unknown operand load mode"); }
 #undef LG_GEMM_CASE
     check_launch("gemm launch");
-    note_launch(ctx, names[args.kernel][a_mode][b_mode]);
+    note_launch(ctx, name);
 }
 
 void launch_reduce(Context* ctx, hipStream_t s, const ReduceArgs& args) {

@@ -1,0 +1,209 @@
+// The software-pipelined fp32 MFMA GEMM for full 128x128 tiles.
+//
+// gemm_f32_pl<AM, BMD, BK, NS>: four waves (2x2, 64x64 each as 2x2 blocks of
+// v_mfma_f32_32x32x2_f32) per 128x128 output tile, operand slices BK deep copied HBM -> LDS by
+// global_load_lds_dwordx4 into NS stages with the layouts and swizzles of gemm_f32_dl. The
+// latency of every step is hidden inside the wave that waits for it, rather than by other
+// waves: with BK = 16 two workgroups share a compute unit (two waves per SIMD), with BK = 32
+// one does (one wave per SIMD).
+//   * A slice's MFMAs come in BK/8 groups of 16 on two alternating fragment register sets; the
+//     fragments of group g + 1 are read from LDS among the MFMAs of group g, the loads of the
+//     slice NS - 1 ahead among those of the first group, at fixed positions
+//     (sched_group_barrier), so each read has most of a group's MFMAs to return in.
+//   * The one barrier per slice sits before the last group's MFMAs, not after them: past it
+//     the wave issues those MFMAs at once (their fragments are already in registers) while the
+//     next slice's first fragments are read, instead of waiting on LDS right after the barrier.
+//   * Stage indices are compile-time constants (the slice loop is unrolled NS times), and
+//     every slice step issues the same loads (past the last slice it loads the last slice again
+//     into a stage no wave reads any more), so each wait on the loads is one constant vmcnt.
+// Requirements, checked by the planner: both operands with a 16-byte aligned unit-stride axis,
+// M and N multiples of 128, every K chunk a multiple of NS * BK. Split-K partials as in
+// gemm_f32_dl. alpha scales the caller's A fragments as they are read (a compile-time branch,
+// chosen per launch), so every product is (alpha*a)*b.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "gemm_dlds.h"
+
+namespace lg {
+namespace gemm_detail {
+
+// LDS read instructions per fragment group of a wave: one 128-bit read per K-contiguous 32-row
+// fragment, four 32-bit reads per M/N-contiguous one.
+template <int AM, int BMD, int FM, int FN>
+constexpr int pl_reads() {
+    return (AM == LOAD_K ? FM : 4 * FM) + (BMD == LOAD_K ? FN : 4 * FN);
+}
+
+// Scheduling groups: N times (one MFMA, then PER instructions of kind MASK).
+// Masks of __builtin_amdgcn_sched_group_barrier: 0x008 MFMA, 0x010 VMEM, 0x100 DS read.
+template <int N, int MASK, int PER>
+__device__ inline void pl_after_each_mfma() {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(MASK, PER, 0);
+    }
+}
+
+template <int AM, int BMD, int BK, int NS>
+__global__ __launch_bounds__(256, (NS * BK * 1024 <= 80 * 1024) ? 2 : 1)
+void gemm_f32_pl(GemmArgs p) {
+    static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
+    constexpr int T = 256, R = 128, NW = 4, FM = 2, FN = 2;
+    using GA = DlGeo<R, BK, T>;
+    using GB = DlGeo<R, BK, T>;
+    constexpr int PER = GA::LOADS + GB::LOADS;  // load instructions per slice per thread
+    constexpr int G = BK / 8;                   // fragment groups per slice
+    static_assert(G >= 2 && G % 2 == 0, "groups alternate between two fragment register sets");
+    static_assert(NS >= 2 && (NS - 1) * PER < 64, "stages (vmcnt counts at most 63)");
+    // Reads of one group after the first RM MFMAs of the previous group, RPM after each; the
+    // first group's loads, two after each MFMA, from the tenth MFMA on (earlier positions
+    // measured 2-4 % slower on batched 1024^3 products).
+    constexpr int RD = pl_reads<AM, BMD, FM, FN>();
+    constexpr int RPM = RD > 12 ? 2 : 1;
+    constexpr int RM = (RD + RPM - 1) / RPM;
+    constexpr int VF = RM < 10 ? 10 - RM : 0;
+    static_assert(RM + VF + PER / 2 <= 16, "a group has 16 MFMAs");
+
+    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
+    float* As = smem;
+    float* Bs = smem + NS * GA::ST;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / 2, wn = wave % 2;
+    const int lr = lane & 31, h = lane >> 5;
+
+    uint32_t plane, tm, tn;
+    decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
+    const uint32_t m0 = tm * R, n0 = tn * R;
+    const uint32_t kb = split * p.k_chunk;
+    const uint32_t ktiles = min(p.k - kb, p.k_chunk) / BK;
+    const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
+                     static_cast<int64_t>(kb) * p.a_sk;
+    const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
+                     static_cast<int64_t>(kb) * p.b_sk;
+    const float alpha_a = p.scale_b ? 1.0f : p.alpha;
+    const float alpha_b = p.scale_b ? p.alpha : 1.0f;
+
+    int64_t sa[GA::LOADS], sb[GB::LOADS];
+#pragma unroll
+    for (int i = 0; i < GA::LOADS; ++i) sa[i] = dl_src<AM, R, BK>((i * NW + wave) * 64 + lane, p.a_sm, p.a_sk);
+#pragma unroll
+    for (int i = 0; i < GB::LOADS; ++i) sb[i] = dl_src<BMD, R, BK>((i * NW + wave) * 64 + lane, p.b_sn, p.b_sk);
+    const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
+    const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
+    // Slice kt into `stage`.
+    auto issue = [&](uint32_t kt, int stage) {
+        float* as = As + stage * GA::ST;
+        float* bs = Bs + stage * GB::ST;
+#pragma unroll
+        for (int i = 0; i < GA::LOADS; ++i) dl_copy16(A + sa[i] + kt * a_step, as + (i * NW + wave) * 256);
+#pragma unroll
+        for (int i = 0; i < GB::LOADS; ++i) dl_copy16(B + sb[i] + kt * b_step, bs + (i * NW + wave) * 256);
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    auto run = [&](auto scale) {
+        constexpr bool SCALE = decltype(scale)::value;
+        floatx4 fa[2][FM], fb[2][FN];
+        // Fragment group g of the slice in `stage` into register set `set`.
+        auto read = [&](int set, int g, int stage) {
+            dl_frag<AM, R, BK, FM>(fa[set], As + stage * GA::ST, wm * 32 * FM, g, lr, h);
+            dl_frag<BMD, R, BK, FN>(fb[set], Bs + stage * GB::ST, wn * 32 * FN, g, lr, h);
+            if constexpr (SCALE) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[set][i] = fa[set][i] * alpha_a;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[set][j] = fb[set][j] * alpha_b;
+            }
+        };
+        // Slices 0 .. NS-2 in flight; slice step kt then issues slice kt + NS - 1 into the
+        // stage slice kt - 1 used (clamped to the last slice), so at the barrier of step kt the
+        // loads issued after slice kt + 1's are always those of the NS - 2 slices behind it.
+#pragma unroll
+        for (int s = 0; s + 1 < NS; ++s) issue(min(static_cast<uint32_t>(s), ktiles - 1), s);
+        wait_vm<(NS - 2) * PER>();
+        __builtin_amdgcn_s_barrier();
+        read(0, 0, 0);
+        for (uint32_t k0 = 0; k0 < ktiles; k0 += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+                const uint32_t kt = k0 + u;
+#pragma unroll
+                for (int g = 0; g + 1 < G; ++g) {
+                    read((g + 1) & 1, g + 1, u);
+                    if (g == 0) issue(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                    mfma_group<FM, FN>(acc, fa[g & 1], fb[g & 1]);
+                    pl_after_each_mfma<RM, 0x100, RPM>();
+                    if (g == 0) {
+                        if constexpr (VF > 0) __builtin_amdgcn_sched_group_barrier(0x008, VF, 0);
+                        pl_after_each_mfma<PER / 2, 0x010, 2>();
+                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - VF - PER / 2, 0);
+                    } else {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // Slice kt + 1 landed for every wave, slice kt read by every wave.
+                wait_vm<(NS - 2) * PER>();
+                wait_lgkm0();
+                __builtin_amdgcn_s_barrier();
+                constexpr int L = (G - 1) & 1;
+                read(0, 0, (u + 1) % NS);  // past the last slice: unused
+                mfma_group<FM, FN>(acc, fa[L], fb[L]);
+                pl_after_each_mfma<RM, 0x100, RPM>();
+                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    if (alpha_a != 1.0f || alpha_b != 1.0f) {
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
+    }
+
+    // Epilogue as gemm_f32_dl's, every element inside the output.
+    if (p.partial != nullptr) {
+        float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = m0 + wm * 32 * FM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                    const uint32_t col = n0 + wn * 32 * FN + j * 32 + lr;
+                    P[static_cast<int64_t>(row) * p.n + col] = acc[i][j][r];
+                }
+        return;
+    }
+    float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + wm * 32 * FM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                const uint32_t col = n0 + wn * 32 * FN + j * 32 + lr;
+                float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
+                float v = acc[i][j][r];
+                if (p.beta != 0.0f) v = p.beta * *q + v;
+                *q = v;
+            }
+}
+
+}  // namespace gemm_detail
+}  // namespace lg

@@ -140,10 +140,17 @@ enum GemmKernel : uint32_t {
     KERN_SMALL = 1,  // gemm_f32_small: one 32x32 tile per workgroup, sixteen waves split K
     KERN_WAVE = 2,   // gemm_f32_wave: one 32x32 tile per wave, four tiles per workgroup
     KERN_OUTER = 3,  // outer_f32: K <= OUTER_MAX_K on the VALU, four outputs per thread
-    KERN_DIRECT = 4  // gemm_f32_dl: 128x128 or 128x256 tiles, slices loaded straight into LDS
+    KERN_DIRECT = 4, // gemm_f32_dl: 128x128 or 128x256 tiles, slices loaded straight into LDS
+    KERN_PIPE = 5    // gemm_f32_pl: full 128x128 tiles, software-pipelined direct loads
 };
 // N extent of the wide direct-load tile (eight waves, 128x256).
 constexpr uint32_t GEMM_WIDE_N = 256;
+// KERN_PIPE: K chunks are whole multiples of PIPE_K_STEP (four 16-deep slices); products of
+// (K, K) operands with chunks of at least PIPE_DEEP_K in whole PIPE_DEEP_STEPs take 32-deep
+// slices, one workgroup per compute unit.
+constexpr uint32_t PIPE_K_STEP = 64;
+constexpr uint32_t PIPE_DEEP_K = 4096;
+constexpr uint32_t PIPE_DEEP_STEP = 128;
 constexpr uint32_t OUTER_MAX_K = 8;
 
 struct GemmArgs {

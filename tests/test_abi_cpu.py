@@ -315,7 +315,17 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_gemm(1.0, dense([2048, 2048]), dense([2048, 2048]), 0.0, dense([2048, 2048]))
     assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (128, 128), 2)
     p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 4096]), 0.0, dense([4096, 4096]))
-    assert (p["tile"], p["kgroups"]) == ((128, 256), 1)
+    assert (p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == ("pipelined", (128, 128), 1, 1024)
+    # The pipelined kernel needs full 128x128 tiles and K in whole 64-deep steps; otherwise
+    # the 128x256 direct-load tile serves grids this large.
+    for m, n, k in [(4000, 4096, 4096), (4096, 4096, 4000), (4096, 4000, 4096)]:
+        p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
+        assert (p["kernel"], p["tile"]) == ("direct", (128, 256)), (m, n, k, p)
+    # 512 full tiles are enough (two workgroups per compute unit); 256 are not.
+    p = C.plan_gemm(1.0, dense([4096, 64]), dense([64, 2048]), 0.0, dense([4096, 2048]))
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (128, 128), 512)
+    p = C.plan_gemm(1.0, dense([2048, 64]), dense([64, 2048]), 0.0, dense([2048, 2048]))
+    assert p["kernel"] != "pipelined"
 
 
 def test_contraction_plans_for_the_baseline_configs():
@@ -329,13 +339,14 @@ def test_contraction_plans_for_the_baseline_configs():
     p = C.plan_contract(1.0, (dense([32, 1024, 1024]), "bik"), (bview, "bkj"), 0.0,
                         (dense([32, 1024, 1024]), "bij"))
     assert p["kind"] == "tiled" and p["batch"] == 32 and p["b_mode"] == "k" and p["a_mode"] == "k"
-    # 1024 tiles of 128x256 fill the chip: the wide direct-load tile.
-    assert (p["kernel"], p["tile"], p["workgroups"]) == ("direct", (128, 256), 32 * 8 * 4)
+    # 2048 full 128x128 tiles: the pipelined kernel.
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (128, 128), 32 * 8 * 8)
     # Config 4: tall K goes split-K with a fixed chunk grid.
     p = C.plan_gemm(1.0, dense([256, 65536]), dense([65536, 256]), 0.0, dense([256, 256]))
     assert p["kind"] == "split" and p["splits"] > 1 and p["k_chunk"] % 32 == 0
-    # Split-K alone fills the chip: 128x128 direct-load tiles, split along K.
-    assert (p["kernel"], p["tile"]) == ("direct", (128, 128))
+    # Split-K alone fills the chip: 128x128 tiles split along K (4 x 128 = 512 workgroups in
+    # chunks of 512), on the pipelined kernel.
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (128, 128), 512)
     assert p["splits"] * p["k_chunk"] >= 65536 > (p["splits"] - 1) * p["k_chunk"]
     assert p["scratch_bytes"] == p["splits"] * 256 * 256 * 4
     # Config 5: transpose_matrix views (strides [1, rows]) are read in place.
@@ -343,11 +354,11 @@ def test_contraction_plans_for_the_baseline_configs():
     Wt = L.TensorView(W.buffer, 0, [16384, 4096], [1, 16384])
     Xt = L.TensorView(X.buffer, 0, [4096, 4096], [1, 4096])
     p = C.plan_gemm(1.0, X, W, 0.0, dense([4096, 16384]))
-    assert p["kind"] == "tiled" and p["tile"] == (128, 256) and p["workgroups"] == 32 * 64
+    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "pipelined", (128, 128), 32 * 128)
     p = C.plan_gemm(1.0, dY, Wt, 0.0, dense([4096, 4096]))
-    assert (p["a_mode"], p["b_mode"]) == ("k", "k")
+    assert (p["a_mode"], p["b_mode"], p["kernel"]) == ("k", "k", "pipelined")
     p = C.plan_gemm(1.0, Xt, dY, 1.0, dense([4096, 16384]))
-    assert (p["a_mode"], p["b_mode"]) == ("mn", "mn")
+    assert (p["a_mode"], p["b_mode"], p["kernel"]) == ("mn", "mn", "pipelined")
 
 
 def test_contraction_plan_kinds_and_edge_semantics():

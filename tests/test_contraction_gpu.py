@@ -835,3 +835,34 @@ def test_four_wave_groups_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
     assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
     _gemm_fast_check(f"four groups {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(4096, 2048, 192, False, False, False),
+                                            (4096, 2048, 128, True, False, False),
+                                            (2048, 4096, 256, False, True, True),
+                                            (4096, 2048, 64, True, True, False),
+                                            (4096, 2048, 4224, False, True, False)])
+def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc):
+    """Grids of 512 full 128x128 tiles on the software-pipelined kernel: every operand layout
+    ((K, MN), (MN, MN), (MN, K) and, with C column-major, the swapped product), alpha != 1
+    (fragments scaled as they are read) with beta != 0, K of one pipeline step (64) and of
+    several, and (K, K) operands with K >= 4096 (32-deep slices, K = 4224: 132 slices), against
+    crates/cpu on every element; the same bits over two runs."""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(7700 + m + n + k)
+    alpha, beta = (1.0, 0.0) if not (ta or tc) else (0.75, -0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"]) == \
+        ("pipelined", (128, 128), 1, 512), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"pipelined {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
