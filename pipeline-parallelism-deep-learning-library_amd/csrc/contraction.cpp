@@ -873,18 +873,33 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             t.kgroups = 4;
         }
     }
-    // Full 128x128 tiles, K chunks in whole pipeline steps and at least two workgroups per
-    // compute unit: the software-pipelined kernel, 128x128 tiles also where 128x256 ones were
-    // chosen (4096^3: 137 -> 142 TFLOP/s; config 3 134 -> 138; config 4 106 -> 111; config
-    // 5 137.5 -> 142).
+    // Full 128x128 tiles with K chunks in whole pipeline steps take the software-pipelined
+    // kernel: with at least two workgroups per compute unit on 16-deep slices, 128x128 tiles
+    // also where 128x256 ones were chosen (4096^3: 137 -> 142.5 TFLOP/s; config 3 134 -> 137;
+    // config 4 106 -> 112; config 5 137.5 -> 143), and 32-deep slices for (K, K) operands with
+    // chunks of at least PIPE_DEEP_K (config 5's dX: 140 -> 145); with one workgroup per compute
+    // unit on 32-deep slices, in place of two wave groups (2048^3: 119 -> 135).
+    t.slice_k = 0;
     const uint32_t last_chunk = k - (splits - 1) * chunk;
-    if (t.kernel == KERN_DIRECT && t.kgroups == 1 && t.tile == GEMM_BM && mm % GEMM_BM == 0 &&
-        nn % GEMM_BN == 0 && chunk % PIPE_K_STEP == 0 && last_chunk % PIPE_K_STEP == 0 &&
-        static_cast<uint64_t>(mm / GEMM_BM) * (nn / GEMM_BN) * batch * splits >= 2 * GEMM_CUS) {
-        t.kernel = KERN_PIPE;
-        t.tile_n = GEMM_BN;
-        t.tiles_n = nn / GEMM_BN;
-        info.tile_n = GEMM_BN;
+    const bool full = mm % GEMM_BM == 0 && nn % GEMM_BN == 0;
+    auto whole = [&](uint32_t bk) {
+        return chunk % (PIPE_STAGES * bk) == 0 && last_chunk % (PIPE_STAGES * bk) == 0;
+    };
+    const uint64_t tiles128 = full ? static_cast<uint64_t>(mm / GEMM_BM) * (nn / GEMM_BN) * batch * splits : 0;
+    if (t.kernel == KERN_DIRECT && t.tile == GEMM_BM && full) {
+        if (t.kgroups == 1 && tiles128 >= 2 * GEMM_CUS && whole(16)) {
+            const bool deep = a_mode == LOAD_K && b_mode == LOAD_K && chunk >= PIPE_DEEP_K && whole(32);
+            t.slice_k = deep ? 32 : 16;
+        } else if (t.kgroups == 2 && whole(32)) {
+            t.slice_k = 32;
+            t.kgroups = 1;
+        }
+        if (t.slice_k != 0) {
+            t.kernel = KERN_PIPE;
+            t.tile_n = GEMM_BN;
+            t.tiles_n = nn / GEMM_BN;
+            info.tile_n = GEMM_BN;
+        }
     }
     info.kgroups = t.kgroups;
     info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE

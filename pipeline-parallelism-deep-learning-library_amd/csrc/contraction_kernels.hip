@@ -323,16 +323,16 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         }
     } else if (a.kernel == KERN_PIPE) {
         if constexpr (AM != LOAD_S && BMD != LOAD_S) {
+            const uint32_t step = PIPE_STAGES * a.slice_k;
             const uint32_t last = a.k - (a.splits - 1) * a.k_chunk;
             if (a.tile != GEMM_BM || a.tile_n != GEMM_BN || a.m % GEMM_BM != 0 || a.n % GEMM_BN != 0 ||
-                a.k_chunk % PIPE_K_STEP != 0 || last % PIPE_K_STEP != 0) {
+                (a.slice_k != 16 && a.slice_k != 32) || a.k_chunk % step != 0 || last % step != 0) {
                 fail_invalid("the pipelined GEMM needs full 128x128 tiles and K chunks in whole steps");
             }
-            if (AM == LOAD_K && BMD == LOAD_K && a.k_chunk >= PIPE_DEEP_K &&
-                a.k_chunk % PIPE_DEEP_STEP == 0 && last % PIPE_DEEP_STEP == 0) {
-                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 32, 4>), dim3(groups), dim3(256), 0, s, a);
+            if (a.slice_k == 32) {
+                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 32, PIPE_STAGES>), dim3(groups), dim3(256), 0, s, a);
             } else {
-                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 16, 4>), dim3(groups), dim3(256), 0, s, a);
+                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 16, PIPE_STAGES>), dim3(groups), dim3(256), 0, s, a);
             }
         } else {
             fail_invalid("the pipelined GEMM needs a unit-stride axis in both operands");
@@ -403,12 +403,12 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
          {"gemm_f32_pl<MN,K>", "gemm_f32_pl<MN,MN>", "gemm_f32_pl<MN,S>"},
          {"gemm_f32_pl<S,K>", "gemm_f32_pl<S,MN>", "gemm_f32_pl<S,S>"}}};
     if (args.kernel > KERN_PIPE) fail_invalid("unknown GEMM kernel");
-    const char* name = names[args.kernel][a_mode][b_mode];
-    if (args.kernel == KERN_PIPE && a_mode == LOAD_K && b_mode == LOAD_K &&
-        args.k_chunk >= PIPE_DEEP_K && args.k_chunk % PIPE_DEEP_STEP == 0 &&
-        (args.k - (args.splits - 1) * args.k_chunk) % PIPE_DEEP_STEP == 0) {
-        name = "gemm_f32_pl32<K,K>";
-    }
+    static const char* const deep[3][3] = {
+        {"gemm_f32_pl32<K,K>", "gemm_f32_pl32<K,MN>", "gemm_f32_pl32<K,S>"},
+        {"gemm_f32_pl32<MN,K>", "gemm_f32_pl32<MN,MN>", "gemm_f32_pl32<MN,S>"},
+        {"gemm_f32_pl32<S,K>", "gemm_f32_pl32<S,MN>", "gemm_f32_pl32<S,S>"}};
+    const char* name = args.kernel == KERN_PIPE && args.slice_k == 32 ? deep[a_mode][b_mode]
+                                                                       : names[args.kernel][a_mode][b_mode];
 #define LG_GEMM_CASE(AMV, BMV)                       \
     if (a_mode == AMV && b_mode == BMV) {            \
         launch_gemm_t<AMV, BMV>(s, args, groups);    \

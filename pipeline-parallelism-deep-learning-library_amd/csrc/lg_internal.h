@@ -145,12 +145,10 @@ enum GemmKernel : uint32_t {
 };
 // N extent of the wide direct-load tile (eight waves, 128x256).
 constexpr uint32_t GEMM_WIDE_N = 256;
-// KERN_PIPE: K chunks are whole multiples of PIPE_K_STEP (four 16-deep slices); products of
-// (K, K) operands with chunks of at least PIPE_DEEP_K in whole PIPE_DEEP_STEPs take 32-deep
-// slices, one workgroup per compute unit.
-constexpr uint32_t PIPE_K_STEP = 64;
-constexpr uint32_t PIPE_DEEP_K = 4096;
-constexpr uint32_t PIPE_DEEP_STEP = 128;
+// KERN_PIPE: K chunks are whole multiples of four slices of `slice_k` (16: two workgroups per
+// compute unit; 32: one).
+constexpr uint32_t PIPE_STAGES = 4;
+constexpr uint32_t PIPE_DEEP_K = 4096;  // (K, K) chunks from this long take 32-deep slices
 constexpr uint32_t OUTER_MAX_K = 8;
 
 struct GemmArgs {
@@ -178,6 +176,8 @@ struct GemmArgs {
     // KERN_DIRECT: wave groups per workgroup that take the tile's K slices in halves and add
     // their sums in group order at the end (1 or 2).
     uint32_t kgroups;
+    // KERN_PIPE: K depth of one LDS slice, 16 or 32.
+    uint32_t slice_k;
 };
 
 // Dot products (M = N = 1): C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k]. Split along K

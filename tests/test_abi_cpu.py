@@ -256,7 +256,7 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_contract(1.0, (t(2048, 2048), "mk"), (t(2048, 2048), "kn"), 0.0,
                         (t(2048, 2048), "mn"))
     assert p["swapped"] and (p["a_mode"], p["b_mode"]) == ("k", "mn")
-    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "direct", (128, 128), 256)
+    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "pipelined", (128, 128), 256)
     # "batched 4096 x 32^3": one 32x32 tile per wave, four per workgroup.
     p = C.plan_contract(1.0, (dense([4096, 32, 32]), "bmk"), (dense([4096, 32, 32]), "bkn"), 0.0,
                         (dense([4096, 32, 32]), "bmn"))
@@ -313,7 +313,12 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_gemm(1.0, dense([1024, 1024]), dense([1024, 1024]), 0.0, dense([1024, 1024]))
     assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (64, 64), 4)
     p = C.plan_gemm(1.0, dense([2048, 2048]), dense([2048, 2048]), 0.0, dense([2048, 2048]))
-    assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (128, 128), 2)
+    assert (p["kind"], p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == \
+        ("tiled", "pipelined", (128, 128), 1, 256)
+    # K not in whole steps of four 32-deep slices, or ragged tiles: two wave groups.
+    for m, n, k in [(2048, 2048, 1936), (2040, 2048, 2048)]:
+        p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
+        assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (128, 128), 2)
     p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 4096]), 0.0, dense([4096, 4096]))
     assert (p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == ("pipelined", (128, 128), 1, 1024)
     # The pipelined kernel needs full 128x128 tiles and K in whole 64-deep steps; otherwise

@@ -777,15 +777,16 @@ def test_wide_direct_load_batched_with_permuted_b(ctx, pool):
         assert float(err.max()) <= 1e-5 * np.sqrt(k) * 0.5 + 1e-5, (bi, float(err.max()))
 
 
-@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2048, 2048, 2048, False, False, False),
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2048, 2048, 1936, False, False, False),
                                             (1952, 2040, 1004, True, False, False),
                                             (2040, 1932, 300, False, True, True),
                                             (2048, 1924, 260, True, True, False)])
 def test_two_wave_groups_per_workgroup(ctx, pool, m, n, k, ta, tb, tc):
     """Grids of exactly 256 128x128 direct-load tiles (one workgroup per compute unit) run two
     wave groups per workgroup, each on half of the K slices, their sums added in group order:
-    ragged M and N edges, odd slice counts (the second group one slice short: K = 1004, 63
-    slices; K = 260, 17), partial last slices (K = 1004, 300, 260), every operand layout, and C
+    ragged M and N edges, K not in whole steps of the pipelined kernel (K = 1936), odd slice
+    counts (the second group one slice short: K = 1004, 63 slices; K = 260, 17), partial last
+    slices (K = 1004, 300, 260), every operand layout, and C
     column-major, against crates/cpu on every element; the same bits over two runs."""
     pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
     la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
@@ -841,13 +842,16 @@ def test_four_wave_groups_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
                                             (4096, 2048, 128, True, False, False),
                                             (2048, 4096, 256, False, True, True),
                                             (4096, 2048, 64, True, True, False),
-                                            (4096, 2048, 4224, False, True, False)])
+                                            (4096, 2048, 4224, False, True, False),
+                                            (2048, 2048, 2048, False, False, False),
+                                            (2048, 2048, 1152, True, True, True)])
 def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc):
-    """Grids of 512 full 128x128 tiles on the software-pipelined kernel: every operand layout
-    ((K, MN), (MN, MN), (MN, K) and, with C column-major, the swapped product), alpha != 1
-    (fragments scaled as they are read) with beta != 0, K of one pipeline step (64) and of
-    several, and (K, K) operands with K >= 4096 (32-deep slices, K = 4224: 132 slices), against
-    crates/cpu on every element; the same bits over two runs."""
+    """Full 128x128 tiles on the software-pipelined kernel. Grids of 512 tiles (16-deep
+    slices): every operand layout ((K, MN), (MN, MN), (MN, K) and, with C column-major, the
+    swapped product), alpha != 1 (fragments scaled as they are read) with beta != 0, K of one
+    pipeline step (64) and of several, and (K, K) operands with K >= 4096 (32-deep slices,
+    K = 4224: 132 slices). Grids of 256 tiles (one workgroup per compute unit, 32-deep
+    slices), also swapped. Against crates/cpu on every element; the same bits over two runs."""
     pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
     la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
     g = rng(7700 + m + n + k)
@@ -856,7 +860,7 @@ def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc):
     Cc = Tensor.random(pool, lc, g)
     plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
     assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"]) == \
-        ("pipelined", (128, 128), 1, 512), plan
+        ("pipelined", (128, 128), 1, m * n // (128 * 128)), plan
     c0 = Cc.host.copy()
     C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
     first = Cc.read().copy()
