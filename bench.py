@@ -876,7 +876,7 @@ def main() -> int:
                             "traffic": traffic_from_profile("gemm4096"),
                             "kernel": ", ".join(head.get("kernels", [])) + " (A K-contiguous, B "
                                       "N-contiguous, %dx%d tiles)" % tuple(head["plan"]["tile"]),
-                            "profile": "profiles/gemm_f32_dl_gemm4096.md, profiles/traffic_gemm4096.txt",
+                            "profile": "profiles/gemm_f32_pl_gemm4096.md, profiles/traffic_gemm4096.txt",
                             "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
     if head and "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
