@@ -18,6 +18,7 @@ namespace {
 
 using gemm_detail::gemm_f32_dl;
 using gemm_detail::gemm_f32_mfma;
+using gemm_detail::gemm_f32_kw;
 using gemm_detail::gemm_f32_pl;
 using gemm_detail::gemm_f32_small;
 using gemm_detail::gemm_f32_wave;
@@ -323,8 +324,17 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         }
     } else if (a.kernel == KERN_PIPE) {
         if constexpr (AM != LOAD_S && BMD != LOAD_S) {
-            const uint32_t step = PIPE_STAGES * a.slice_k;
             const uint32_t last = a.k - (a.splits - 1) * a.k_chunk;
+            if (a.tile == GEMM_SMALL_TILE) {
+                const uint32_t step = PIPE_KW * PIPE_STAGES * 16;
+                if (a.tile_n != GEMM_SMALL_TILE || a.m % GEMM_SMALL_TILE != 0 || a.n % GEMM_SMALL_TILE != 0 ||
+                    a.slice_k != 16 || a.k_chunk % step != 0 || last % step != 0) {
+                    fail_invalid("the K-split GEMM needs full 64x64 tiles and K chunks in whole steps");
+                }
+                hipLaunchKernelGGL((gemm_f32_kw<AM, BMD, 16, PIPE_STAGES>), dim3(groups), dim3(256), 0, s, a);
+                return;
+            }
+            const uint32_t step = PIPE_STAGES * a.slice_k;
             if (a.tile != GEMM_BM || a.tile_n != GEMM_BN || a.m % GEMM_BM != 0 || a.n % GEMM_BN != 0 ||
                 (a.slice_k != 16 && a.slice_k != 32) || a.k_chunk % step != 0 || last % step != 0) {
                 fail_invalid("the pipelined GEMM needs full 128x128 tiles and K chunks in whole steps");
@@ -407,8 +417,16 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
         {"gemm_f32_pl32<K,K>", "gemm_f32_pl32<K,MN>", "gemm_f32_pl32<K,S>"},
         {"gemm_f32_pl32<MN,K>", "gemm_f32_pl32<MN,MN>", "gemm_f32_pl32<MN,S>"},
         {"gemm_f32_pl32<S,K>", "gemm_f32_pl32<S,MN>", "gemm_f32_pl32<S,S>"}};
-    const char* name = args.kernel == KERN_PIPE && args.slice_k == 32 ? deep[a_mode][b_mode]
-                                                                       : names[args.kernel][a_mode][b_mode];
+    static const char* const kw[3][3] = {
+        {"gemm_f32_kw<K,K>", "gemm_f32_kw<K,MN>", "gemm_f32_kw<K,S>"},
+        {"gemm_f32_kw<MN,K>", "gemm_f32_kw<MN,MN>", "gemm_f32_kw<MN,S>"},
+        {"gemm_f32_kw<S,K>", "gemm_f32_kw<S,MN>", "gemm_f32_kw<S,S>"}};
+    const char* name = names[args.kernel][a_mode][b_mode];
+    if (args.kernel == KERN_PIPE && args.tile == GEMM_SMALL_TILE) {
+        name = kw[a_mode][b_mode];
+    } else if (args.kernel == KERN_PIPE && args.slice_k == 32) {
+        name = deep[a_mode][b_mode];
+    }
 #define LG_GEMM_CASE(AMV, BMV)                       \
     if (a_mode == AMV && b_mode == BMV) {            \
         launch_gemm_t<AMV, BMV>(s, args, groups);    \

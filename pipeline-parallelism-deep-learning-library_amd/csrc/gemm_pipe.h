@@ -1,4 +1,5 @@
-// The software-pipelined fp32 MFMA GEMM for full 128x128 tiles.
+// The software-pipelined fp32 MFMA GEMMs: gemm_f32_pl for full 128x128 tiles and, below it,
+// gemm_f32_kw for full 64x64 tiles whose waves split K.
 //
 // gemm_f32_pl<AM, BMD, BK, NS>: four waves (2x2, 64x64 each as 2x2 blocks of
 // v_mfma_f32_32x32x2_f32) per 128x128 output tile, operand slices BK deep copied HBM -> LDS by
@@ -203,6 +204,172 @@ void gemm_f32_pl(GemmArgs p) {
                 if (p.beta != 0.0f) v = p.beta * *q + v;
                 *q = v;
             }
+}
+
+// gemm_f32_kw<AM, BMD, BK, NS>: a 64x64 output tile per workgroup whose four waves each
+// compute the whole tile (2x2 blocks of 32x32) over a quarter of the K chunk, through their own
+// NS LDS stages filled by their own direct loads: no barrier inside the loop (each wave waits
+// only for its own loads), the same in-wave pipelining as gemm_f32_pl. The four sums meet
+// through LDS at the end in a fixed order, (s0 + s1) + (s2 + s3), each wave adding and storing
+// one 32x32 block. One workgroup per compute unit (128 KB of stages): for grids of about one
+// 64x64 tile per compute unit (1024^3: 75 -> 97-99 TFLOP/s against four wave groups of four
+// waves sharing stages). Full 64x64 tiles, K chunks in whole multiples of 4 * NS * BK.
+template <int AM, int BMD, int BK, int NS>
+__global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
+    constexpr int R = 64, FM = 2, FN = 2, W = 4;
+    using GA = DlGeo<R, BK, 64>;
+    using GB = DlGeo<R, BK, 64>;
+    constexpr int PER = GA::LOADS + GB::LOADS;
+    constexpr int G = BK / 8;
+    static_assert(G >= 2 && G % 2 == 0, "groups alternate between two fragment register sets");
+    static_assert(NS >= 2 && (NS - 1) * PER < 64, "stages");
+    constexpr int RD = pl_reads<AM, BMD, FM, FN>();
+    constexpr int RPM = RD > 12 ? 2 : 1;
+    constexpr int RM = (RD + RPM - 1) / RPM;
+    constexpr int VF = RM < 10 ? 10 - RM : 0;
+    constexpr int VPM = PER / 4;  // loads after each of four MFMAs
+    static_assert(RM + VF + 4 <= 16, "a group has 16 MFMAs");
+    constexpr int WST = NS * (GA::ST + GB::ST);
+    static_assert(W * WST >= W * FM * FN * 16 * 64, "the sums fit in the stages");
+    __shared__ __attribute__((aligned(16))) float smem[W * WST];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, h = lane >> 5;
+    float* As = smem + wave * WST;
+    float* Bs = As + NS * GA::ST;
+
+    uint32_t plane, tm, tn;
+    decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
+    const uint32_t m0 = tm * R, n0 = tn * R;
+    const uint32_t kb = split * p.k_chunk;
+    const uint32_t per = min(p.k - kb, p.k_chunk) / W;
+    const uint32_t ktiles = per / BK;
+    const uint32_t k0w = kb + wave * per;
+    const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
+                     static_cast<int64_t>(k0w) * p.a_sk;
+    const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
+                     static_cast<int64_t>(k0w) * p.b_sk;
+    const float alpha_a = p.scale_b ? 1.0f : p.alpha;
+    const float alpha_b = p.scale_b ? p.alpha : 1.0f;
+
+    int64_t sa[GA::LOADS], sb[GB::LOADS];
+#pragma unroll
+    for (int i = 0; i < GA::LOADS; ++i) sa[i] = dl_src<AM, R, BK>(i * 64 + lane, p.a_sm, p.a_sk);
+#pragma unroll
+    for (int i = 0; i < GB::LOADS; ++i) sb[i] = dl_src<BMD, R, BK>(i * 64 + lane, p.b_sn, p.b_sk);
+    const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
+    const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
+    auto issue = [&](uint32_t kt, int stage) {
+        float* as = As + stage * GA::ST;
+        float* bs = Bs + stage * GB::ST;
+#pragma unroll
+        for (int i = 0; i < GA::LOADS; ++i) dl_copy16(A + sa[i] + kt * a_step, as + i * 256);
+#pragma unroll
+        for (int i = 0; i < GB::LOADS; ++i) dl_copy16(B + sb[i] + kt * b_step, bs + i * 256);
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    auto run = [&](auto scale) {
+        constexpr bool SCALE = decltype(scale)::value;
+        floatx4 fa[2][FM], fb[2][FN];
+        auto read = [&](int set, int g, int stage) {
+            dl_frag<AM, R, BK, FM>(fa[set], As + stage * GA::ST, 0, g, lr, h);
+            dl_frag<BMD, R, BK, FN>(fb[set], Bs + stage * GB::ST, 0, g, lr, h);
+            if constexpr (SCALE) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[set][i] = fa[set][i] * alpha_a;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[set][j] = fb[set][j] * alpha_b;
+            }
+        };
+#pragma unroll
+        for (int s = 0; s + 1 < NS; ++s) issue(min(static_cast<uint32_t>(s), ktiles - 1), s);
+        wait_vm<(NS - 2) * PER>();
+        read(0, 0, 0);
+        for (uint32_t k0 = 0; k0 < ktiles; k0 += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+                const uint32_t kt = k0 + u;
+#pragma unroll
+                for (int g = 0; g + 1 < G; ++g) {
+                    read((g + 1) & 1, g + 1, u);
+                    if (g == 0) issue(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                    mfma_group<FM, FN>(acc, fa[g & 1], fb[g & 1]);
+                    pl_after_each_mfma<RM, 0x100, RPM>();
+                    if (g == 0) {
+                        if constexpr (VF > 0) __builtin_amdgcn_sched_group_barrier(0x008, VF, 0);
+                        pl_after_each_mfma<4, 0x010, VPM>();
+                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - VF - 4, 0);
+                    } else {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                wait_vm<(NS - 2) * PER>();  // slice kt + 1 landed (this wave's own loads)
+                constexpr int L = (G - 1) & 1;
+                read(0, 0, (u + 1) % NS);
+                mfma_group<FM, FN>(acc, fa[L], fb[L]);
+                pl_after_each_mfma<RM, 0x100, RPM>();
+                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    if (alpha_a != 1.0f || alpha_b != 1.0f) {
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
+    }
+
+    // The four sums meet through LDS: wave w adds block w of every wave's sum as
+    // (s0 + s1) + (s2 + s3) and stores it.
+    wait_vm<0>();
+    __syncthreads();
+    {
+        float* mine = smem + wave * (FM * FN * 16 * 64) + lane;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mine[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+    }
+    __syncthreads();
+    const int bi_ = wave >> 1, bj = wave & 1;
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float* q = smem + ((bi_ * FN + bj) * 16 + r) * 64 + lane;
+        constexpr int S = FM * FN * 16 * 64;
+        v[r] = (q[0] + q[S]) + (q[2 * S] + q[3 * S]);
+    }
+    if (p.partial != nullptr) {
+        float* P = p.partial + static_cast<int64_t>(plane) * p.m * p.n;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = m0 + bi_ * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+            const uint32_t col = n0 + bj * 32 + lr;
+            P[static_cast<int64_t>(row) * p.n + col] = v[r];
+        }
+        return;
+    }
+    float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t row = m0 + bi_ * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        const uint32_t col = n0 + bj * 32 + lr;
+        float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
+        float x = v[r];
+        if (p.beta != 0.0f) x = p.beta * *q + x;
+        *q = x;
+    }
 }
 
 }  // namespace gemm_detail

@@ -141,13 +141,15 @@ enum GemmKernel : uint32_t {
     KERN_WAVE = 2,   // gemm_f32_wave: one 32x32 tile per wave, four tiles per workgroup
     KERN_OUTER = 3,  // outer_f32: K <= OUTER_MAX_K on the VALU, four outputs per thread
     KERN_DIRECT = 4, // gemm_f32_dl: 128x128 or 128x256 tiles, slices loaded straight into LDS
-    KERN_PIPE = 5    // gemm_f32_pl: full 128x128 tiles, software-pipelined direct loads
+    KERN_PIPE = 5    // gemm_f32_pl (full 128x128 tiles) / gemm_f32_kw (full 64x64 tiles): software-pipelined direct loads
 };
 // N extent of the wide direct-load tile (eight waves, 128x256).
 constexpr uint32_t GEMM_WIDE_N = 256;
 // KERN_PIPE: K chunks are whole multiples of four slices of `slice_k` (16: two workgroups per
-// compute unit; 32: one).
+// compute unit; 32: one), on 128x128 tiles; on 64x64 tiles four waves each take a quarter of
+// every chunk (K chunks in whole multiples of 4 * PIPE_STAGES * 16).
 constexpr uint32_t PIPE_STAGES = 4;
+constexpr uint32_t PIPE_KW = 4;  // waves splitting K on 64x64 tiles
 constexpr uint32_t PIPE_DEEP_K = 4096;  // (K, K) chunks from this long take 32-deep slices
 constexpr uint32_t OUTER_MAX_K = 8;
 

@@ -311,7 +311,13 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
         p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
         assert (p["kind"], p["tile"]) == ("split", (128, 128)), (m, n, k, p)
     p = C.plan_gemm(1.0, dense([1024, 1024]), dense([1024, 1024]), 0.0, dense([1024, 1024]))
-    assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (64, 64), 4)
+    assert (p["kind"], p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == \
+        ("tiled", "pipelined", (64, 64), 4, 256)
+    # Ragged 64x64 tiles, or K chunks not in whole steps of four waves x four 16-deep slices:
+    # four wave groups sharing stages on the direct-load kernel.
+    for m, n, k in [(1000, 1024, 1024), (1024, 1024, 1000)]:
+        p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
+        assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (64, 64), 4)
     p = C.plan_gemm(1.0, dense([2048, 2048]), dense([2048, 2048]), 0.0, dense([2048, 2048]))
     assert (p["kind"], p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == \
         ("tiled", "pipelined", (128, 128), 1, 256)

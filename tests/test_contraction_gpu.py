@@ -808,14 +808,15 @@ def test_two_wave_groups_per_workgroup(ctx, pool, m, n, k, ta, tb, tc):
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
-@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(1024, 1024, 1024, False, False, False),
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(1024, 1024, 1000, False, False, False),
                                             (1000, 1020, 900, True, False, False),
                                             (1020, 968, 1000, False, True, True),
                                             (964, 1024, 516, True, True, False)])
 def test_four_wave_groups_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
     """Grids of exactly 256 64x64 tiles (a 128x128 grid would need split-K) on the direct-load
-    kernel with four wave groups of 32-deep slices: ragged edges, groups with fewer slices
-    than the others (K = 900: 8, 8, 8, 5 slices; K = 516: 5, 5, 5, 2), partial last slices,
+    kernel with four wave groups of 32-deep slices: ragged edges, K not in whole steps of the
+    K-split kernel (K = 1000), groups with fewer slices than the others (K = 900: 8, 8, 8, 5
+    slices; K = 516: 5, 5, 5, 2), partial last slices,
     every operand layout and C column-major, against crates/cpu on every element; the same
     bits over two runs."""
     pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
@@ -835,6 +836,36 @@ def test_four_wave_groups_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
     C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
     assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
     _gemm_fast_check(f"four groups {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(1024, 1024, 1024, False, False, False),
+                                            (1024, 1024, 512, True, False, False),
+                                            (1024, 1024, 768, False, True, True),
+                                            (1024, 1024, 1536, True, True, False)])
+def test_k_split_waves_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
+    """Grids of 256 full 64x64 tiles on the kernel whose four waves each take a quarter of K
+    through their own stages (K = 512: eight 16-deep slices per wave, one loop pass of four
+    stages twice): every operand layout, with C column-major the swapped product, alpha != 1
+    with beta != 0, against crates/cpu on every element; the same bits over two runs (the four
+    quarter sums are added in a fixed order)."""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(7800 + m + n + k)
+    alpha, beta = (1.0, 0.0) if not (ta or tc) else (-0.75, 0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"]) == \
+        ("pipelined", (64, 64), 4, 256), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"k-split waves {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
