@@ -909,6 +909,29 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             info.tile_n = GEMM_BN;
         }
     }
+    // Split-K products of at most GEMM_CUS / 2 full 64x64 tiles (short outputs, long K) take the
+    // K-split-wave kernel on 64x64 tiles instead, split to about one workgroup per compute unit
+    // in chunks of whole steps: fewer, longer splits (config 4: 16 of 4096 instead of 128 of
+    // 512 on 128x128 tiles, 4 MiB of partials instead of 32; 112 -> 116 TFLOP/s).
+    const uint32_t kw_step = PIPE_KW * PIPE_STAGES * 16;
+    if (t.kernel == KERN_PIPE && t.tile == GEMM_BM && splits > 1 && full64 && k % kw_step == 0) {
+        const uint64_t t64 = static_cast<uint64_t>(mm / GEMM_SMALL_TILE) * (nn / GEMM_SMALL_TILE) * batch;
+        if (t64 <= GEMM_CUS / 2) {
+            uint64_t s64 = GEMM_CUS / t64;
+            const uint64_t c64 = ((k + s64 - 1) / s64 + kw_step - 1) / kw_step * kw_step;
+            s64 = (k + c64 - 1) / c64;
+            if (s64 > 1 && s64 * split_bytes <= SPLIT_PARTIAL_MAX) {
+                t.tile = t.tile_n = GEMM_SMALL_TILE;
+                t.tiles_m = mm / GEMM_SMALL_TILE;
+                t.tiles_n = nn / GEMM_SMALL_TILE;
+                info.tile_m = info.tile_n = GEMM_SMALL_TILE;
+                splits = static_cast<uint32_t>(s64);
+                chunk = static_cast<uint32_t>(c64);
+                t.kgroups = PIPE_KW;
+                t.slice_k = 16;
+            }
+        }
+    }
     info.kgroups = t.kgroups;
     info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
                   : t.kernel == KERN_PIPE   ? LG_KERNEL_PIPELINED

@@ -355,11 +355,17 @@ def test_contraction_plans_for_the_baseline_configs():
     # Config 4: tall K goes split-K with a fixed chunk grid.
     p = C.plan_gemm(1.0, dense([256, 65536]), dense([65536, 256]), 0.0, dense([256, 256]))
     assert p["kind"] == "split" and p["splits"] > 1 and p["k_chunk"] % 32 == 0
-    # Split-K alone fills the chip: 128x128 tiles split along K (4 x 128 = 512 workgroups in
-    # chunks of 512), on the pipelined kernel.
-    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (128, 128), 512)
+    # Split-K alone fills the chip: 16 64x64 tiles whose four waves each take a quarter of every
+    # K chunk, split 16 ways in chunks of 4096 (256 workgroups, 4 MiB of partials).
+    assert (p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == ("pipelined", (64, 64), 4, 256)
+    assert (p["splits"], p["k_chunk"]) == (16, 4096)
     assert p["splits"] * p["k_chunk"] >= 65536 > (p["splits"] - 1) * p["k_chunk"]
     assert p["scratch_bytes"] == p["splits"] * 256 * 256 * 4
+    # Outputs of more than 128 64x64 tiles keep 128x128 tiles; K not in whole steps of 256
+    # keeps the 128x128 split.
+    for m, n, k in [(1024, 1024, 65536), (256, 256, 65536 - 64)]:
+        p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
+        assert p["kind"] == "split" and p["tile"] == (128, 128), (m, n, k, p)
     # Config 5: transpose_matrix views (strides [1, rows]) are read in place.
     X, W, dY = dense([4096, 4096]), dense([4096, 16384]), dense([4096, 16384])
     Wt = L.TensorView(W.buffer, 0, [16384, 4096], [1, 16384])

@@ -869,6 +869,36 @@ def test_k_split_waves_on_64x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
+@pytest.mark.parametrize("m,n,k,ta,tb,tc,splits", [(512, 512, 16384, True, False, False, 4),
+                                                   (256, 512, 8192, False, True, True, 8),
+                                                   (256, 256, 16384, True, True, False, 16)])
+def test_k_split_waves_split_along_k(ctx, pool, m, n, k, ta, tb, tc, splits):
+    """Short outputs with long K: 64x64 tiles of the K-split-wave kernel, split along K to about
+    one workgroup per compute unit, partials added in split order by the reduction: (MN, MN),
+    the swapped (K, K) product with C column-major, (MN, K) with 16 splits of 1024; alpha != 1,
+    beta != 0; against crates/cpu on every element, the same bits over two runs. (With inputs
+    uniform on [-1, 1], K stays at most 16384: both sides accumulate in f32, and for longer K
+    their rounding alone approaches the bound.)"""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(7900 + m + n + k)
+    alpha, beta = 0.75, -0.5
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kind"], plan["kernel"], plan["tile"], plan["splits"], plan["workgroups"]) == \
+        ("split", "pipelined", (64, 64), splits, 256), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"k-split waves, split {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
 @pytest.mark.parametrize("m,n,k,ta,tb,tc", [(4096, 2048, 192, False, False, False),
                                             (4096, 2048, 128, True, False, False),
                                             (2048, 4096, 256, False, True, True),
