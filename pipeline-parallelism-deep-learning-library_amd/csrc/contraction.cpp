@@ -909,6 +909,25 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             info.tile_n = GEMM_BN;
         }
     }
+    // Grids of 128x64 tiles that fill three workgroups per compute unit in one round (more
+    // than 2 * GEMM_CUS, at most 3 * GEMM_CUS), where 128x128 tiles would leave many compute
+    // units with one tile and others with two: 128x64 tiles on the pipelined kernel, three
+    // workgroups per compute unit (the rank-4 48^6 product, 2304^3: 324 tiles of 128x128 or
+    // 648 of 128x64; 97 -> 116 TFLOP/s against 64x64 tiles).
+    const uint64_t tiles_n64 = static_cast<uint64_t>(mm / GEMM_BM) * (nn / PIPE_NARROW_N) * batch;
+    if ((t.kernel == KERN_DIRECT || t.kernel == KERN_TILE) && t.slice_k == 0 && t.kgroups == 1 &&
+        splits == 1 && a_mode != LOAD_S && b_mode != LOAD_S && mm % GEMM_BM == 0 &&
+        nn % PIPE_NARROW_N == 0 && chunk % (PIPE_STAGES * 16) == 0 && tiles_n64 > 2 * GEMM_CUS &&
+        tiles_n64 <= 3 * GEMM_CUS) {
+        t.kernel = KERN_PIPE;
+        t.slice_k = 16;
+        t.tile = GEMM_BM;
+        t.tile_n = PIPE_NARROW_N;
+        t.tiles_m = mm / GEMM_BM;
+        t.tiles_n = nn / PIPE_NARROW_N;
+        info.tile_m = GEMM_BM;
+        info.tile_n = PIPE_NARROW_N;
+    }
     // Split-K products of at most GEMM_CUS / 2 full 64x64 tiles (short outputs, long K) take the
     // K-split-wave kernel on 64x64 tiles instead, split to about one workgroup per compute unit
     // in chunks of whole steps: fewer, longer splits (config 4: 16 of 4096 instead of 128 of

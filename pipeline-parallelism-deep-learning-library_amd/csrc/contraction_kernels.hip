@@ -335,6 +335,14 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
                 return;
             }
             const uint32_t step = PIPE_STAGES * a.slice_k;
+            if (a.tile_n == PIPE_NARROW_N) {
+                if (a.tile != GEMM_BM || a.m % GEMM_BM != 0 || a.n % PIPE_NARROW_N != 0 || a.slice_k != 16 ||
+                    a.k_chunk % step != 0 || last % step != 0) {
+                    fail_invalid("the pipelined GEMM needs full 128x64 tiles and K chunks in whole steps");
+                }
+                hipLaunchKernelGGL((gemm_f32_pl<AM, BMD, 16, PIPE_STAGES, 1>), dim3(groups), dim3(256), 0, s, a);
+                return;
+            }
             if (a.tile != GEMM_BM || a.tile_n != GEMM_BN || a.m % GEMM_BM != 0 || a.n % GEMM_BN != 0 ||
                 (a.slice_k != 16 && a.slice_k != 32) || a.k_chunk % step != 0 || last % step != 0) {
                 fail_invalid("the pipelined GEMM needs full 128x128 tiles and K chunks in whole steps");
@@ -421,8 +429,14 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
         {"gemm_f32_kw<K,K>", "gemm_f32_kw<K,MN>", "gemm_f32_kw<K,S>"},
         {"gemm_f32_kw<MN,K>", "gemm_f32_kw<MN,MN>", "gemm_f32_kw<MN,S>"},
         {"gemm_f32_kw<S,K>", "gemm_f32_kw<S,MN>", "gemm_f32_kw<S,S>"}};
+    static const char* const narrow[3][3] = {
+        {"gemm_f32_pl_n64<K,K>", "gemm_f32_pl_n64<K,MN>", "gemm_f32_pl_n64<K,S>"},
+        {"gemm_f32_pl_n64<MN,K>", "gemm_f32_pl_n64<MN,MN>", "gemm_f32_pl_n64<MN,S>"},
+        {"gemm_f32_pl_n64<S,K>", "gemm_f32_pl_n64<S,MN>", "gemm_f32_pl_n64<S,S>"}};
     const char* name = names[args.kernel][a_mode][b_mode];
-    if (args.kernel == KERN_PIPE && args.tile == GEMM_SMALL_TILE) {
+    if (args.kernel == KERN_PIPE && args.tile == GEMM_BM && args.tile_n == PIPE_NARROW_N) {
+        name = narrow[a_mode][b_mode];
+    } else if (args.kernel == KERN_PIPE && args.tile == GEMM_SMALL_TILE) {
         name = kw[a_mode][b_mode];
     } else if (args.kernel == KERN_PIPE && args.slice_k == 32) {
         name = deep[a_mode][b_mode];

@@ -50,25 +50,36 @@ __device__ inline void pl_after_each_mfma() {
     }
 }
 
-template <int AM, int BMD, int BK, int NS>
-__global__ __launch_bounds__(256, (NS * BK * 1024 <= 80 * 1024) ? 2 : 1)
+// Workgroups of gemm_f32_pl per compute unit, by LDS (160 KB), at most three.
+template <int BK, int NS, int FN>
+constexpr int pl_workgroups() {
+    constexpr int by_lds = 160 * 1024 / (NS * BK * 4 * (128 + 64 * FN));
+    return by_lds < 3 ? by_lds : 3;
+}
+
+template <int AM, int BMD, int BK, int NS, int FN = 2>
+__global__ __launch_bounds__(256, (pl_workgroups<BK, NS, FN>()))
 void gemm_f32_pl(GemmArgs p) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
-    constexpr int T = 256, R = 128, NW = 4, FM = 2, FN = 2;
-    using GA = DlGeo<R, BK, T>;
-    using GB = DlGeo<R, BK, T>;
+    static_assert(FN == 1 || FN == 2, "128x64 or 128x128 tiles");
+    constexpr int T = 256, NW = 4, FM = 2, RA = 128, RB = 64 * FN;
+    using GA = DlGeo<RA, BK, T>;
+    using GB = DlGeo<RB, BK, T>;
     constexpr int PER = GA::LOADS + GB::LOADS;  // load instructions per slice per thread
     constexpr int G = BK / 8;                   // fragment groups per slice
+    constexpr int MG = 4 * FM * FN;             // MFMAs per group
     static_assert(G >= 2 && G % 2 == 0, "groups alternate between two fragment register sets");
     static_assert(NS >= 2 && (NS - 1) * PER < 64, "stages (vmcnt counts at most 63)");
     // Reads of one group after the first RM MFMAs of the previous group, RPM after each; the
-    // first group's loads, two after each MFMA, from the tenth MFMA on (earlier positions
-    // measured 2-4 % slower on batched 1024^3 products).
+    // first group's loads, up to two after each of NV MFMAs, from the tenth MFMA on where the
+    // group is that long (earlier positions measured 2-4 % slower on batched 1024^3 products).
     constexpr int RD = pl_reads<AM, BMD, FM, FN>();
-    constexpr int RPM = RD > 12 ? 2 : 1;
+    constexpr int RPM = RD > MG * 3 / 4 ? 2 : 1;
     constexpr int RM = (RD + RPM - 1) / RPM;
-    constexpr int VF = RM < 10 ? 10 - RM : 0;
-    static_assert(RM + VF + PER / 2 <= 16, "a group has 16 MFMAs");
+    constexpr int NV = (PER + 1) / 2;
+    constexpr int VF0 = 10 - RM < MG - RM - NV ? 10 - RM : MG - RM - NV;
+    constexpr int VF = VF0 > 0 ? VF0 : 0;
+    static_assert(RM + VF + NV <= MG, "MFMAs of a group");
 
     __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
     float* As = smem;
@@ -80,7 +91,7 @@ void gemm_f32_pl(GemmArgs p) {
     uint32_t plane, tm, tn;
     decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
     const uint32_t bi = plane / p.splits, split = plane - bi * p.splits;
-    const uint32_t m0 = tm * R, n0 = tn * R;
+    const uint32_t m0 = tm * RA, n0 = tn * RB;
     const uint32_t kb = split * p.k_chunk;
     const uint32_t ktiles = min(p.k - kb, p.k_chunk) / BK;
     const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
@@ -92,9 +103,9 @@ void gemm_f32_pl(GemmArgs p) {
 
     int64_t sa[GA::LOADS], sb[GB::LOADS];
 #pragma unroll
-    for (int i = 0; i < GA::LOADS; ++i) sa[i] = dl_src<AM, R, BK>((i * NW + wave) * 64 + lane, p.a_sm, p.a_sk);
+    for (int i = 0; i < GA::LOADS; ++i) sa[i] = dl_src<AM, RA, BK>((i * NW + wave) * 64 + lane, p.a_sm, p.a_sk);
 #pragma unroll
-    for (int i = 0; i < GB::LOADS; ++i) sb[i] = dl_src<BMD, R, BK>((i * NW + wave) * 64 + lane, p.b_sn, p.b_sk);
+    for (int i = 0; i < GB::LOADS; ++i) sb[i] = dl_src<BMD, RB, BK>((i * NW + wave) * 64 + lane, p.b_sn, p.b_sk);
     const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
     const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
     // Slice kt into `stage`.
@@ -120,8 +131,8 @@ void gemm_f32_pl(GemmArgs p) {
         floatx4 fa[2][FM], fb[2][FN];
         // Fragment group g of the slice in `stage` into register set `set`.
         auto read = [&](int set, int g, int stage) {
-            dl_frag<AM, R, BK, FM>(fa[set], As + stage * GA::ST, wm * 32 * FM, g, lr, h);
-            dl_frag<BMD, R, BK, FN>(fb[set], Bs + stage * GB::ST, wn * 32 * FN, g, lr, h);
+            dl_frag<AM, RA, BK, FM>(fa[set], As + stage * GA::ST, wm * 32 * FM, g, lr, h);
+            dl_frag<BMD, RB, BK, FN>(fb[set], Bs + stage * GB::ST, wn * 32 * FN, g, lr, h);
             if constexpr (SCALE) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i) fa[set][i] = fa[set][i] * alpha_a;
@@ -149,10 +160,10 @@ void gemm_f32_pl(GemmArgs p) {
                     pl_after_each_mfma<RM, 0x100, RPM>();
                     if (g == 0) {
                         if constexpr (VF > 0) __builtin_amdgcn_sched_group_barrier(0x008, VF, 0);
-                        pl_after_each_mfma<PER / 2, 0x010, 2>();
-                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - VF - PER / 2, 0);
+                        pl_after_each_mfma<NV, 0x010, 2>();
+                        __builtin_amdgcn_sched_group_barrier(0x008, MG - RM - VF - NV, 0);
                     } else {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, MG - RM, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -164,7 +175,7 @@ void gemm_f32_pl(GemmArgs p) {
                 read(0, 0, (u + 1) % NS);  // past the last slice: unused
                 mfma_group<FM, FN>(acc, fa[L], fb[L]);
                 pl_after_each_mfma<RM, 0x100, RPM>();
-                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, MG - RM, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }

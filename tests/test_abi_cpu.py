@@ -290,8 +290,13 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_contract(1.0, (dense([48] * 4), "ijkl"), (dense([48] * 4), "klmn"), 0.0,
                         (dense([48] * 4), "ijmn"))
     assert (p["kind"], p["groups"], p["m"], p["n"], p["k"]) == ("tiled", 1, 2304, 2304, 2304)
-    # 324 tiles of 128x128 spread unevenly over 256 compute units: 64x64 tiles (1296).
-    assert (p["tile"], p["workgroups"]) == ((64, 64), 1296)
+    # 324 tiles of 128x128 spread unevenly over 256 compute units: 648 128x64 tiles fill three
+    # pipelined workgroups per compute unit in one round.
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (128, 64), 648)
+    # Not full 128x64 tiles, or K not in whole 64-deep steps: 64x64 tiles (1296).
+    for m, n, k in [(2300, 2304, 2304), (2304, 2304, 2000)]:
+        p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
+        assert (p["tile"], p["workgroups"]) == ((64, 64), 1296), (m, n, k, p)
     # Batched dot products (no split once the batch fills the chip) and a skinny output.
     p = C.plan_contract(1.0, (dense([4096, 1, 512]), "bmk"), (dense([4096, 512, 1]), "bkn"), 0.0,
                         (dense([4096, 1, 1]), "bmn"))

@@ -899,6 +899,35 @@ def test_k_split_waves_split_along_k(ctx, pool, m, n, k, ta, tb, tc, splits):
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2304, 2304, 256, False, False, False),
+                                            (2048, 3072, 128, True, False, False),
+                                            (3072, 2048, 192, False, True, True),
+                                            (2304, 2304, 64, True, True, False)])
+def test_pipelined_128x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
+    """Grids of 648-768 full 128x64 tiles (three pipelined workgroups per compute unit in one
+    round): (K, MN), (MN, MN), the swapped (K, K) product with C column-major, (MN, K) with K of
+    one pipeline step; alpha != 1 with beta != 0; against crates/cpu on every element, the same
+    bits over two runs."""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(8000 + m + n + k)
+    alpha, beta = (1.0, 0.0) if not (ta or tc) else (0.75, -0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kernel"], plan["tile"], plan["workgroups"]) == \
+        ("pipelined", (128, 64), m * n // (128 * 64)), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"pipelined 128x64 {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
 @pytest.mark.parametrize("m,n,k,ta,tb,tc", [(4096, 2048, 192, False, False, False),
                                             (4096, 2048, 128, True, False, False),
                                             (2048, 4096, 256, False, True, True),
