@@ -899,6 +899,33 @@ def test_k_split_waves_split_along_k(ctx, pool, m, n, k, ta, tb, tc, splits):
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
+@pytest.mark.parametrize("m,n,k,ta,tb,tc,splits", [(1024, 1024, 16384, False, True, False, 8),
+                                                   (1024, 2048, 8192, True, False, True, 4)])
+def test_pipelined_kernel_split_along_k(ctx, pool, m, n, k, ta, tb, tc, splits):
+    """Split-K on the pipelined 128x128 kernel (outputs too large for the 64x64 K-split
+    waves): raw partials in chunks of 2048, added in split order by the reduction; (K, K) and,
+    with C column-major, the swapped product; against crates/cpu on every element, the same
+    bits over two runs."""
+    pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
+    la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
+    g = rng(8100 + m + n + k)
+    alpha, beta = (1.0, 0.0) if not tc else (0.75, -0.5)
+    A, B = Tensor.random(pool, la, g), Tensor.random(pool, lb, g)
+    Cc = Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
+    assert (plan["kind"], plan["kernel"], plan["tile"], plan["splits"], plan["workgroups"]) == \
+        ("split", "pipelined", (128, 128), splits, 512), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    _gemm_fast_check(f"pipelined split {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
+                     B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
 @pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2304, 2304, 256, False, False, False),
                                             (2048, 3072, 128, True, False, False),
                                             (3072, 2048, 192, False, True, True),

@@ -22,12 +22,13 @@ from linalg_hip import _native as N
 pytestmark = pytest.mark.gpu
 
 SHAPES = [
-    (256, 256, 65536),  # split-K, 128 splits: the full 32 MiB of partials
-    (64, 48, 30000),    # 32x32 tiles of sixteen waves, split along K
+    (384, 384, 65536),  # split-K on 128x128 tiles, 56 splits: 31.5 MiB of partials
+    (256, 256, 65536),  # split-K on 64x64 K-split-wave tiles, 16 splits
+    (64, 48, 30000),    # one 64x64 register-staged tile, split 209 ways along K
     (1, 1, 1 << 20),    # split dot
     (1, 1, 100003),     # a smaller split dot
     (300, 200, 100),    # one tiled launch, no scratch
-    (256, 128, 9000),   # split-K again, fewer and smaller partials
+    (256, 128, 9000),   # split-K again on 64x64 tiles, fewer and smaller partials
 ]
 
 
