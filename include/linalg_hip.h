@@ -428,7 +428,8 @@ typedef struct lg_contract_plan {
     uint32_t swapped;     /* 1 when C is contiguous along M and is computed as C^T = B^T.A^T */
     uint32_t kgroups;     /* LG_KERNEL_DIRECT: wave groups per workgroup splitting the tile's K
                              slices when the grid leaves at most one workgroup per compute unit
-                             (2 for 128x128 tiles, 4 for 64x64), else 1 */
+                             (2 for 128x128 tiles, 4 for 64x64); LG_KERNEL_PIPELINED on 64x64
+                             tiles: 4 (each wave takes a quarter of every K chunk); else 1 */
     uint32_t reserved;
 } lg_contract_plan;
 
