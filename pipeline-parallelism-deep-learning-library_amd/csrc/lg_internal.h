@@ -287,11 +287,14 @@ constexpr uint32_t PERM_MAX_RANK = 8;  // MAX_RANK, src/ops/permutation.rs:14-16
 constexpr uint32_t PERM_TILE_A = 64;   // transpose tile extent along a (source unit stride)
 constexpr uint32_t PERM_TILE_B = 64;   // transpose tile extent along b (destination unit stride)
 // Streaming configuration, used when source + destination exceed the 256 MiB Infinity Cache
-// (nothing of the operands survives in cache between uses, so accesses are non-temporal and
-// tiles are twice as long along the source rows).
-constexpr uint32_t PERM_STREAM_TILE_A = 128;
+// (nothing of the operands survives in cache between uses, so accesses are non-temporal):
+// 64 x 256 tiles of 1024 threads, so each destination row segment a tile writes is 1 KiB, as
+// long as one wave's 128-bit store.
+constexpr uint32_t PERM_STREAM_TILE_A = 64;
+constexpr uint32_t PERM_STREAM_TILE_B = 256;
+constexpr uint32_t PERM_STREAM_THREADS = 1024;
 constexpr uint64_t PERM_STREAM_BYTES = 256ull << 20;
-constexpr uint32_t PERM_THREADS = 256;         // copy kernel and streaming transpose tiles
+constexpr uint32_t PERM_THREADS = 256;         // copy kernel
 constexpr uint32_t PERM_CACHED_THREADS = 512;  // transpose tiles that stay in the cache
 
 struct PermTileArgs {

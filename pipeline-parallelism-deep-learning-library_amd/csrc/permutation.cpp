@@ -221,8 +221,9 @@ Gather plan_gather(lg_elem elem, const View& src, const View& dst, bool conj_req
     const uint64_t moved = 2 * dst.len() * e.bytes;
     g.info.streaming = (vec && moved > PERM_STREAM_BYTES) ? 1 : 0;
     const uint32_t tile_a = g.info.streaming ? PERM_STREAM_TILE_A : PERM_TILE_A;
+    const uint32_t tile_b = g.info.streaming ? PERM_STREAM_TILE_B : PERM_TILE_B;
     p.tiles_a = static_cast<uint32_t>((shape[a] + tile_a - 1) / tile_a);
-    p.tiles_b = static_cast<uint32_t>((shape[b] + PERM_TILE_B - 1) / PERM_TILE_B);
+    p.tiles_b = static_cast<uint32_t>((shape[b] + tile_b - 1) / tile_b);
     p.total_tiles = static_cast<uint64_t>(p.tiles_a) * p.tiles_b * outer_count;
     g.info.vector = vec ? 1 : 0;
     g.info.workgroups = perm_tile_workgroups(p.total_tiles);

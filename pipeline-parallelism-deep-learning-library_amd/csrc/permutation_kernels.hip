@@ -75,13 +75,16 @@ __global__ __launch_bounds__(PERM_THREADS) void perm_copy(PermCopyArgs p) {
 constexpr uint64_t TILE_GRID_CAP = 1u << 22;
 constexpr uint64_t COPY_GRID_CAP = 1u << 20;
 
-// Streaming (operands beyond the Infinity Cache) tiles run 256 threads, cached ones 512:
-// measured best on configs 2b and 2a respectively (6.05 vs 5.8 TB/s; 6.44 vs 6.21 TB/s).
+// Streaming (operands beyond the Infinity Cache) tiles are 64 x 256 with 1024 threads, cached
+// ones 64 x 64 with 512: measured best on configs 2b and 2a respectively (2b: 6.14 TB/s against
+// 6.0 for 128 x 64 tiles of 256 threads, whose destination row segments are 256 B; the 1 GiB
+// tensor [1024,1024,256] 5.89 against 5.62. 2a: 6.44 against 6.21 with 256 threads).
 template <int W, bool CONJ, bool VEC, int TA, bool NT>
 void tile_t(hipStream_t s, const PermTileArgs& a) {
-    constexpr int threads = NT ? PERM_THREADS : PERM_CACHED_THREADS;
+    constexpr int threads = NT ? PERM_STREAM_THREADS : PERM_CACHED_THREADS;
+    constexpr int TB = NT ? PERM_STREAM_TILE_B : PERM_TILE_B;
     const uint64_t g = perm_tile_workgroups(a.total_tiles);
-    hipLaunchKernelGGL((perm_tile<W, CONJ, VEC, TA, PERM_TILE_B, NT ? 3 : 0, threads>),
+    hipLaunchKernelGGL((perm_tile<W, CONJ, VEC, TA, TB, NT ? 3 : 0, threads>),
                        dim3(static_cast<uint32_t>(g)), dim3(threads), 0, s, a);
 }
 

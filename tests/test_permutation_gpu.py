@@ -363,6 +363,25 @@ def test_baseline_configs_full_size_bit_exact(ctx, pool, shape, perm, seed):
     assert np.array_equal(back_buf.read(np.uint32, count=n), x.view(np.uint32))
 
 
+def test_streaming_transposes_with_ragged_edges_and_complex_words(ctx, pool):
+    """Permutations moving more than 256 MiB take the streaming tiles (non-temporal accesses,
+    their own tile shape; rows a multiple of 16 bytes, as 128-bit access needs): ragged edges
+    along both tile axes under a batch axis (f32), a complex transpose (two-word elements) and a
+    complex adjoint applied twice (sign flip, then back), each against the gathered words."""
+    for dtype, shape, perm in [("f32", [3, 4100, 5004], [0, 2, 1]), ("c64", [4098, 4102], [1, 0])]:
+        src_buf = pool.alloc(dtype, int(np.prod(shape)))
+        view = P.permute_view(L.TensorView.row_major(src_buf, 0, shape, dtype), perm)
+        dst = L.TensorView.row_major(pool.alloc(dtype, view.len()), 0, view.shape, dtype)
+        plan = P.plan("materialize", view, dst)
+        assert plan["kind"] == "tile" and plan["streaming"], (dtype, plan)
+        pool.free_all()
+    check_materialize(ctx, pool, "f32", [3, 4100, 5004], [0, 2, 1], 0, None, 0, 1400)
+    pool.free_all()
+    check_materialize(ctx, pool, "c64", [4098, 4102], [1, 0], 0, None, 0, 1401)
+    pool.free_all()
+    check_involution(ctx, pool, "c64", [2], 2900, 2902, 1402)
+
+
 def test_transpose_reads_misaligned_rows_to_the_edges_of_the_buffer(ctx, pool):
     """A view whose rows are not 16-byte aligned, in a buffer that starts 4 bytes into a device
     allocation and ends at the view's last word: interior and edge tiles move every word once
