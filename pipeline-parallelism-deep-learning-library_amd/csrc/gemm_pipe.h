@@ -1,15 +1,15 @@
-// The software-pipelined fp32 MFMA GEMMs: gemm_f32_pl for full 128x128 tiles and, below it,
-// gemm_f32_kw for full 64x64 tiles whose waves split K.
+// The software-pipelined fp32 MFMA GEMMs: gemm_f32_pl for full 128x128 and 128x64 tiles and,
+// below it, gemm_f32_kw for full 64x64 tiles whose waves split K.
 //
-// gemm_f32_pl<AM, BMD, BK, NS>: four waves (2x2, 64x64 each as 2x2 blocks of
-// v_mfma_f32_32x32x2_f32) per 128x128 output tile, operand slices BK deep copied HBM -> LDS by
-// global_load_lds_dwordx4 into NS stages with the layouts and swizzles of gemm_f32_dl. The
+// gemm_f32_pl<AM, BMD, BK, NS, FN>: four waves (2x2, each 64 x 32*FN as 2 x FN blocks of
+// v_mfma_f32_32x32x2_f32) per 128 x 64*FN output tile, operand slices BK deep copied HBM -> LDS
+// by global_load_lds_dwordx4 into NS stages with the layouts and swizzles of gemm_f32_dl. The
 // latency of every step is hidden inside the wave that waits for it, rather than by other
-// waves: with BK = 16 two workgroups share a compute unit (two waves per SIMD), with BK = 32
-// one does (one wave per SIMD).
-//   * A slice's MFMAs come in BK/8 groups of 16 on two alternating fragment register sets; the
-//     fragments of group g + 1 are read from LDS among the MFMAs of group g, the loads of the
-//     slice NS - 1 ahead among those of the first group, at fixed positions
+// waves: with BK = 16 two 128x128 workgroups (or three 128x64 ones) share a compute unit, with
+// BK = 32 one 128x128 workgroup does (one wave per SIMD).
+//   * A slice's MFMAs come in BK/8 groups of 8 * FN on two alternating fragment register sets;
+//     the fragments of group g + 1 are read from LDS among the MFMAs of group g, the loads of
+//     the slice NS - 1 ahead among those of the first group, at fixed positions
 //     (sched_group_barrier), so each read has most of a group's MFMAs to return in.
 //   * The one barrier per slice sits before the last group's MFMAs, not after them: past it
 //     the wave issues those MFMAs at once (their fragments are already in registers) while the
@@ -18,7 +18,7 @@
 //     every slice step issues the same loads (past the last slice it loads the last slice again
 //     into a stage no wave reads any more), so each wait on the loads is one constant vmcnt.
 // Requirements, checked by the planner: both operands with a 16-byte aligned unit-stride axis,
-// M and N multiples of 128, every K chunk a multiple of NS * BK. Split-K partials as in
+// M a multiple of 128 and N of 64 * FN, every K chunk a multiple of NS * BK. Split-K partials as in
 // gemm_f32_dl. alpha scales the caller's A fragments as they are read (a compile-time branch,
 // chosen per launch), so every product is (alpha*a)*b.
 #pragma once
@@ -32,8 +32,9 @@
 namespace lg {
 namespace gemm_detail {
 
-// LDS read instructions per fragment group of a wave: one 128-bit read per K-contiguous 32-row
-// fragment, four 32-bit reads per M/N-contiguous one.
+// LDS read instructions per fragment group of a wave, at most: one 128-bit read per
+// K-contiguous 32-row fragment, four 32-bit reads per M/N-contiguous one (which the compiler
+// pairs into two ds_read2st64_b32 where it can; the schedule then has slots to spare).
 template <int AM, int BMD, int FM, int FN>
 constexpr int pl_reads() {
     return (AM == LOAD_K ? FM : 4 * FM) + (BMD == LOAD_K ? FN : 4 * FN);
