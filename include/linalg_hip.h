@@ -259,11 +259,12 @@ typedef struct lg_tensor {
  * operand that is read reaching past its storage. Stores beta*C + alpha*A*B (beta = 0 does
  * not read C, alpha = 0 does not read A or B, K = 0 with beta = 0 stores zeros); every
  * product is (alpha*a)*b, as in the reference's loop, summed in the kernel's fixed order.
- * F16 and BF16 operands compute as CpuBackend::gemm does (crates/cpu/src/lib.rs:270-291,
- * f32 sums stored rounded to the 16-bit type) but sum the exact products in f64 and round
- * once: the reference's known answers (crates/cpu/src/invariants.rs:556-720) hold bit for
- * bit, and elsewhere the result is the 16-bit rounding of a sum at least as accurate as the
- * reference's f32 one. The checks run before `ctx` is used.
+ * F16 and BF16 operands return CpuBackend::gemm's bits (crates/cpu/src/lib.rs:270-291 with
+ * `accumulate`, :664-691): per output, acc = beta*C in f32 (0 when beta is 0), then
+ * acc = acc + (alpha*a)*b in k order, every multiply and add rounded to f32, stored rounded
+ * to the 16-bit type to nearest even (the half crate's from_f32_const); only NaN payloads may
+ * differ. This runs on the vector ALUs (one lane per output), not the matrix cores, whose
+ * summation order is their own. The checks run before `ctx` is used.
  * Enqueues on `stream` (NULL = context stream) and returns before the device finishes, as
  * the GPU backends do (crates/core/src/lib.rs:72-82). On any error nothing is launched. */
 lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_tensor* a, const lg_tensor* b,

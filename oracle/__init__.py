@@ -14,6 +14,8 @@ Functions (C implementations in oracle.c, each citing the reference code it rest
   north_star_tol  max|err| <= 1e-5 * sqrt(K) * max|a| * max|b|
   gemm_seq_16     CpuBackend::gemm on F16 / BF16 tensors: f32 accumulation, one 16-bit
                   rounding per output (crates/cpu/src/lib.rs:270-291, 700-720)
+  f32_to_f16, f16_to_f32
+                  the half crate's (2.7.1) f16 conversions crates/cpu stores and loads with
   gelu, gelu_backward, add_bias, bias_grad, mse_grad, sgd_step, f32_to_bf16, bf16_to_f32
                   the CpuBackend activation and training ops (crates/cpu/src/lib.rs:297-533,
                   722-729, 809-842), sequential, one rounding per operation
@@ -75,9 +77,14 @@ def lib():
                            ("oracle_bias_grad_f32", [vp, vp, u64, u64]),
                            ("oracle_sgd_step_f32", [vp, vp, ctypes.c_float, u64]),
                            ("oracle_f32_to_bf16", [vp, vp, u64]),
-                           ("oracle_bf16_to_f32", [vp, vp, u64])]:
+                           ("oracle_bf16_to_f32", [vp, vp, u64]),
+                           ("oracle_f32_to_f16", [vp, vp, u64]),
+                           ("oracle_f16_to_f32", [vp, vp, u64])]:
             getattr(L, name).argtypes = args
             getattr(L, name).restype = None
+        L.oracle_gemm_seq_16.argtypes = [ctypes.c_int, u64, u64, u64, ctypes.c_float,
+                                         ctypes.c_float, vp, i64, i64, vp, i64, i64, vp, i64, i64]
+        L.oracle_gemm_seq_16.restype = None
         L.oracle_mse_grad_f32.argtypes = [vp, vp, vp, u64]
         L.oracle_mse_grad_f32.restype = ctypes.c_float
         _lib = L
@@ -313,28 +320,43 @@ def bf16_to_f32(h) -> np.ndarray:
 
 
 # ---- f16 contraction: the exact result rounded once ----------------------------------------
+def f32_to_f16(x) -> np.ndarray:
+    """f16::from_f32_const of the half crate 2.7.1 (crates/cpu/src/lib.rs:700-703): the f32
+    bits rounded to nearest even, NaN quiet with its top payload bits; uint16 bits."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32).view(np.uint32))
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def f16_to_f32(h) -> np.ndarray:
+    """f16::to_f32_const (crates/cpu/src/lib.rs:694-697): exact widening of uint16 bits."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32(h.ctypes.data, y.ctypes.data, h.size)
+    return y
+
+
 def gemm_seq_16(kind: str, alpha: float, beta: float, a, b, c) -> np.ndarray:
     """CpuBackend::gemm on F16 or BF16 tensors (crates/cpu/src/lib.rs:270-291 with
     `accumulate`, :664-691): every element widened exactly to f32, acc = beta*C (0 when beta is
     0, C unread), then acc += (alpha*a)*b over k in order in f32 unless alpha is 0, stored
     rounded to the nearest 16-bit value, ties to even (`from_f32_const`, :700-720). a, b, c
-    are uint16 bit arrays [m, k], [k, n], [m, n]; returns the uint16 bits of C."""
-    def widen(h):
-        h = np.asarray(h, dtype=np.uint16)
-        if kind == "f16":
-            return h.view(np.float16).astype(np.float32)
-        return bf16_to_f32(h)
-    a32, b32 = widen(a), widen(b)
-    m, k = a32.shape
-    n = b32.shape[1]
-    acc = np.zeros((m, n), np.float32) if beta == 0.0 else np.float32(beta) * widen(c)
-    if alpha != 0.0:
-        al = np.float32(alpha)
-        for t in range(k):
-            acc = acc + (al * a32[:, t:t + 1]) * b32[t:t + 1, :]
-    if kind == "f16":
-        return acc.astype(np.float16).view(np.uint16)
-    return f32_to_bf16(acc).reshape(m, n)
+    are uint16 bit arrays [m, k], [k, n], [m, n] of any strides; returns the uint16 bits of
+    C (a new dense array; c is not changed)."""
+    if kind not in ("f16", "bf16"):
+        raise ValueError(kind)
+    a = np.asarray(a, dtype=np.uint16)
+    b = np.asarray(b, dtype=np.uint16)
+    out = np.array(c, dtype=np.uint16, order="C", copy=True)
+    m, k = a.shape
+    n = b.shape[1]
+    assert b.shape[0] == k and out.shape == (m, n)
+    lib().oracle_gemm_seq_16(0 if kind == "f16" else 1, m, n, k, alpha, beta,
+                             a.ctypes.data, a.strides[0] // 2, a.strides[1] // 2,
+                             b.ctypes.data, b.strides[0] // 2, b.strides[1] // 2,
+                             out.ctypes.data, n, 1)
+    return out
 
 
 def f16_round_exact(x) -> int:

@@ -434,3 +434,109 @@ void oracle_f32_to_bf16(const uint32_t* x, uint16_t* y, uint64_t n) {
 void oracle_bf16_to_f32(const uint16_t* x, uint32_t* y, uint64_t n) {
     for (uint64_t i = 0; i < n; ++i) y[i] = (uint32_t)x[i] << 16;
 }
+
+/* ---- CpuBackend::gemm on F16 / BF16 tensors -------------------------------------------
+ * crates/cpu loads and stores 16-bit elements through the `half` crate, version 2.7.1
+ * (pinned =2.7.1 by crates/cpu/Cargo.toml:14; not vendored under the reference), with its
+ * `*_const` conversions (crates/cpu/src/lib.rs:694-720). Restated from the crate's published
+ * f16 <-> f32 algorithm:
+ *   f16 -> f32: exact; a NaN keeps sign and payload (shifted up 13) and gets the quiet bit.
+ *   f32 -> f16: round to nearest even on the f32 bits; halves of the subnormal range kept,
+ *     values from 65520 up overflow to infinity, below 2^-25 (and ties at 2^-25) to zero;
+ *     a NaN keeps the sign and the top ten payload bits and gets the quiet bit (0x0200).
+ *   bf16 <-> f32: the high half of the f32 bits, rounded to nearest even, NaN | 0x0040,
+ *     which is oracle_f32_to_bf16 above. */
+static float f16_bits_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0x1f) {
+        bits = sign | 0x7f800000u | (man ? 0x00400000u | (man << 13) : 0u);
+    } else if (exp != 0) {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    } else if (man == 0) {
+        bits = sign;
+    } else {  /* subnormal: man * 2^-24, normalised */
+        int e = -14;
+        uint32_t m = man;
+        while (!(m & 0x400u)) { m <<= 1; --e; }
+        bits = sign | ((uint32_t)(e + 127) << 23) | ((m & 0x3ffu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t oracle_f32_to_f16_bits(uint32_t x) {
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = x & 0x7f800000u, man = x & 0x007fffffu;
+    if (exp == 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (man ? 0x0200u | (man >> 13) : 0u));
+    const int half_exp = (int)(exp >> 23) - 127 + 15;
+    if (half_exp >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    if (half_exp <= 0) {
+        if (14 - half_exp > 24) return (uint16_t)sign;
+        const uint32_t full = man | 0x00800000u;
+        uint32_t half_man = full >> (14 - half_exp);
+        const uint32_t round_bit = 1u << (13 - half_exp);
+        /* ties to even: the round bit and any lower bit or the kept least significant bit */
+        if ((full & round_bit) && (full & (3u * round_bit - 1u))) ++half_man;
+        return (uint16_t)(sign | half_man);
+    }
+    uint32_t out = sign | ((uint32_t)half_exp << 10) | (man >> 13);
+    if ((man & 0x1000u) && (man & 0x2fffu)) ++out;  /* a carry runs into the exponent */
+    return (uint16_t)out;
+}
+
+void oracle_f32_to_f16(const uint32_t* x, uint16_t* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) y[i] = oracle_f32_to_f16_bits(x[i]);
+}
+
+void oracle_f16_to_f32(const uint16_t* x, float* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) y[i] = f16_bits_to_f32(x[i]);
+}
+
+static float widen16(int kind, uint16_t h) {
+    if (kind == 0) return f16_bits_to_f32(h);
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint16_t narrow16(int kind, float v) {
+    uint32_t bits;
+    uint16_t out;
+    memcpy(&bits, &v, 4);
+    if (kind == 0) return oracle_f32_to_f16_bits(bits);
+    oracle_f32_to_bf16(&bits, &out, 1);
+    return out;
+}
+
+/*
+ * CpuBackend::gemm with dtype F16 (kind 0) or BF16 (kind 1): crates/cpu/src/lib.rs:270-291
+ * hands `accumulate` (:664-691) loaders that widen each element to f32 and a store that
+ * rounds the f32 accumulator to 16 bits, so for every (row, col) in row-major order
+ *   acc = (beta == 0) ? +0 : beta * widen(C[row, col])              (C unread when beta is 0)
+ *   if (alpha != 0) for inner in 0..k: acc += (alpha * widen(A[row, inner])) * widen(B[inner, col])
+ *   C[row, col] = narrow(acc)
+ * with every f32 multiply and add rounded on its own. Strides in elements.
+ */
+void oracle_gemm_seq_16(int kind, uint64_t m, uint64_t n, uint64_t k, float alpha, float beta,
+                        const uint16_t* a, int64_t a_rs, int64_t a_cs,
+                        const uint16_t* b, int64_t b_rs, int64_t b_cs,
+                        uint16_t* c, int64_t c_rs, int64_t c_cs) {
+    for (uint64_t row = 0; row < m; ++row) {
+        for (uint64_t col = 0; col < n; ++col) {
+            uint16_t* out = c + (int64_t)row * c_rs + (int64_t)col * c_cs;
+            float acc = (beta == 0.0f) ? 0.0f : beta * widen16(kind, *out);
+            if (alpha != 0.0f) {
+                for (uint64_t inner = 0; inner < k; ++inner) {
+                    const float t = alpha * widen16(kind, a[(int64_t)row * a_rs + (int64_t)inner * a_cs]);
+                    const float p = t * widen16(kind, b[(int64_t)inner * b_rs + (int64_t)col * b_cs]);
+                    acc = acc + p;
+                }
+            }
+            *out = narrow16(kind, acc);
+        }
+    }
+}

@@ -39,6 +39,7 @@ SOURCES = [
     "contraction_f16_kernels.hip",
     "permutation_kernels.hip",
     "training_kernels.hip",
+    "backend_gemm16_kernels.hip",
 ]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

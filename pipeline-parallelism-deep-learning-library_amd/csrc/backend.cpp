@@ -377,6 +377,38 @@ lg_core_error lg_backend_convert(lg_ctx* ctx, void* stream, const lg_tensor* x, 
 
 }  // extern "C"
 
+// CpuBackend::gemm on F16 / BF16 tensors (crates/cpu/src/lib.rs:270-291): the checked
+// row-major or transposed operands, offset 0, handed to the kernel that repeats
+// `accumulate`'s f32 arithmetic per output. A and B are not read when alpha or k is 0.
+static void enqueue_gemm16(lg_ctx* ctx, hipStream_t s, const lg_tensor* a, const lg_tensor* b,
+                           const lg_tensor* c, uint64_t m, uint64_t n, uint64_t k, float alpha,
+                           float beta) {
+    if (m > UINT32_MAX - GEMM16_SEQ_TILE || n > UINT32_MAX - GEMM16_SEQ_TILE || k > UINT32_MAX) {
+        fail_invalid("16-bit gemm extents exceed 2^32 - 129");
+    }
+    Gemm16SeqArgs g{};
+    g.a = static_cast<const uint16_t*>(a->base);
+    g.b = static_cast<const uint16_t*>(b->base);
+    g.c = static_cast<uint16_t*>(c->base);
+    g.a_sm = static_cast<int64_t>(a->strides[0]);
+    g.a_sk = static_cast<int64_t>(a->strides[1]);
+    g.b_sk = static_cast<int64_t>(b->strides[0]);
+    g.b_sn = static_cast<int64_t>(b->strides[1]);
+    g.c_sm = static_cast<int64_t>(c->strides[0]);
+    g.m = static_cast<uint32_t>(m);
+    g.n = static_cast<uint32_t>(n);
+    g.k = static_cast<uint32_t>(k);
+    g.tiles_m = (g.m + GEMM16_SEQ_TILE - 1) / GEMM16_SEQ_TILE;
+    g.tiles_n = (g.n + GEMM16_SEQ_TILE - 1) / GEMM16_SEQ_TILE;
+    g.alpha = alpha;
+    g.beta = beta;
+    g.kind = a->dtype == LG_DTYPE_BF16 ? 1 : 0;
+    g.a_kfast = g.a_sk == 1;
+    g.b_kfast = g.b_sk == 1;
+    set_device(ctx);
+    launch_gemm16_seq(ctx, s, g);
+}
+
 extern "C" lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_tensor* a,
                                          const lg_tensor* b, const lg_tensor* c, float alpha,
                                          float beta) {
@@ -410,8 +442,12 @@ extern "C" lg_core_error lg_backend_gemm(lg_ctx* ctx, void* stream, const lg_ten
             return LG_CORE_OK;
         }
         const lg_status st = guarded([&] {
-            enqueue_gemm_views(ctx, pick_stream(ctx, stream), alpha, to_view(a), to_view(b), beta,
-                               to_view(c), a->dtype);
+            if (a->dtype == LG_DTYPE_F32) {
+                enqueue_gemm_views(ctx, pick_stream(ctx, stream), alpha, to_view(a), to_view(b),
+                                   beta, to_view(c));
+            } else {
+                enqueue_gemm16(ctx, pick_stream(ctx, stream), a, b, c, m, n, k, alpha, beta);
+            }
         });
         if (st != LG_OK) return LG_CORE_UNSUPPORTED_DEVICE;  // launch failure; message kept
         return LG_CORE_OK;

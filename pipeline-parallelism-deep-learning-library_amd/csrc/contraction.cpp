@@ -1137,10 +1137,8 @@ void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg
 }
 
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
-                        float beta, const View& c, uint32_t dtype) {
-    const bool half = dtype != LG_DTYPE_F32;
-    Plan plan = plan_merged(a, b, c, merge_all(groups_from_gemm(a, b, c)), alpha, beta, half);
-    if (dtype == LG_DTYPE_BF16) plan.hgemm.kind = plan.hgeneral.kind = plan.hfill.kind = 1;
+                        float beta, const View& c) {
+    Plan plan = plan_merged(a, b, c, merge_all(groups_from_gemm(a, b, c)), alpha, beta, false);
     set_device(ctx);
     execute(ctx, s, plan);
 }

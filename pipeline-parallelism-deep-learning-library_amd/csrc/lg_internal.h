@@ -266,6 +266,23 @@ struct FillHalfArgs {
     Axes4 c_batch, c_m, c_n;
     uint32_t kind;
 };
+// The Backend's 16-bit gemm with CpuBackend's f32 arithmetic (one lane per output, k in
+// order, one rounding per multiply and add, one 16-bit rounding at the end). Operands are 2-D
+// with element strides; C's column stride is 1. *_kfast: the operand's K stride is 1.
+struct Gemm16SeqArgs {
+    const uint16_t* a;
+    const uint16_t* b;
+    uint16_t* c;
+    int64_t a_sm, a_sk, b_sk, b_sn, c_sm;
+    uint32_t m, n, k, tiles_m, tiles_n;
+    float alpha, beta;
+    uint32_t kind;  // 0 = f16, 1 = bf16
+    uint32_t a_kfast, b_kfast;
+};
+constexpr uint32_t GEMM16_SEQ_TILE = 128;  // square output tile of the kernel
+void launch_gemm16_seq(Context* ctx, hipStream_t s, const Gemm16SeqArgs& args);
+uint64_t gemm16_seq_workgroups(uint32_t m, uint32_t n);
+
 void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int a_mode,
                       int b_mode);
 void launch_general_half(Context* ctx, hipStream_t s, const GeneralHalfArgs& args);
@@ -355,12 +372,11 @@ struct lg_ctx : lg::Context {};
 
 namespace lg {
 void set_device(const lg_ctx* ctx);
-// Plans and enqueues the batched-matrix product C = alpha*A.B + beta*C on views whose ranges
+// Plans and enqueues the f32 matrix product C = alpha*A.B + beta*C on views whose ranges
 // the caller has already checked (the gemm form of the contraction planner; alias rules and
-// the scalar rules apply, views are not re-validated). dtype is an lg_dtype: F32 takes the
-// f32 kernels; F16 and BF16 the 16-bit ones (f64 sums of exact products, one rounding).
+// the scalar rules apply, views are not re-validated).
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,
-                        float beta, const View& c, uint32_t dtype);
+                        float beta, const View& c);
 // Plans C = alpha*A.B + beta*C (the gemm form, f32) and enqueues it on `stream` with device
 // scratch from the caller: once validation and planning have passed, and only when the plan
 // needs scratch, `scratch(ctx)` is called with the context's device current and returns

@@ -429,3 +429,110 @@ def test_gemm_seq_16_reads_nothing_unread_and_sums_in_f32():
     ops = to_16("bf16", [1.0, 2.0 ** -8, 2.0 ** -30]).reshape(1, 3)
     got = oracle.gemm_seq_16("bf16", 1.0, 0.0, ops, to_16("bf16", [1.0] * 3).reshape(3, 1), nan)
     assert int(got[0, 0]) == 0x3F80
+
+
+def test_f32_to_f16_matches_numpy_rounding_on_every_rounding_position():
+    """The half crate's f32 -> f16 (oracle.f32_to_f16) against numpy's IEEE conversion on
+    every finite f32 whose low 13 mantissa bits are a rounding-critical pattern (exact, just
+    below, at and just above the halfway point, all kept-bit parities), for every exponent
+    from far below the f16 subnormals to past the overflow threshold, both signs, every value
+    of the top ten mantissa bits; plus random bit patterns. Covers the subnormal positions,
+    where the round bit moves into the top ten bits, and the carry into the exponent."""
+    low = np.array([0, 1, 0x7FF, 0x800, 0x801, 0xFFF, 0x1000, 0x1001, 0x17FF, 0x1800, 0x1FFF],
+                   np.uint32)
+    top = np.arange(1024, dtype=np.uint32) << 13
+    exps = np.arange(90, 148, dtype=np.uint32) << 23
+    bits = (exps[:, None, None] | top[None, :, None] | low[None, None, :]).ravel()
+    bits = np.concatenate([bits, bits | 0x80000000, np.array([0, 0x80000000, 1, 0x807FFFFF,
+                                                             0x7F800000, 0xFF800000,
+                                                             0x7F7FFFFF, 0x477FF000,
+                                                             0x477FEFFF, 0x33000000,
+                                                             0x33000001], np.uint32)])
+    rnd = np.random.default_rng(16).integers(0, 2 ** 32, 1 << 21, dtype=np.uint64).astype(np.uint32)
+    bits = np.concatenate([bits, rnd[(rnd & 0x7F800000) != 0x7F800000]])
+    got = oracle.f32_to_f16(bits.view(np.float32))
+    with np.errstate(over="ignore"):
+        want = bits.view(np.float32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    # The reference's own asserted bits (crates/cpu/src/invariants.rs:560-564).
+    assert list(oracle.f32_to_f16(np.array([2048, 2050, 2052, 2049, 2051], np.float32))) == \
+        [0x6800, 0x6801, 0x6802, 0x6800, 0x6802]
+    # 65520 is the tie between 65504 and 2^16: ties to even overflow to infinity.
+    assert list(oracle.f32_to_f16(np.array([65504, 65519.996, 65520, -1e9], np.float32))) == \
+        [0x7BFF, 0x7BFF, 0x7C00, 0xFC00]
+
+
+def test_f16_nan_conversions_keep_sign_and_payload_quietly():
+    """The crate's NaN rule, both directions: f32 NaN -> sign | 0x7C00 | 0x0200 | top ten
+    payload bits; f16 NaN -> sign | 0x7FC00000 | payload << 13; infinities stay exact."""
+    f = np.array([0x7F800001, 0x7FC00000, 0xFFFFFFFF, 0x7F802000, 0xFF800000], np.uint32)
+    assert [hex(v) for v in oracle.f32_to_f16(f.view(np.float32))] == \
+        ["0x7e00", "0x7e00", "0xffff", "0x7e01", "0xfc00"]
+    h = np.array([0x7C01, 0x7E00, 0xFFFF, 0x7C00, 0xFC00], np.uint16)
+    assert [hex(v) for v in oracle.f16_to_f32(h).view(np.uint32)] == \
+        ["0x7fc02000", "0x7fc00000", "0xffffe000", "0x7f800000", "0xff800000"]
+
+
+def test_f16_to_f32_is_exact_on_every_finite_half():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = (h & 0x7C00) != 0x7C00
+    got = oracle.f16_to_f32(h[finite])
+    assert np.array_equal(got.view(np.uint32), h[finite].view(np.float16).astype(np.float32).view(np.uint32))
+
+
+# Closed forms where the evaluation order decides the bits (same layout as GEMM_16_KATS).
+# k order: 2^-14 + 2048 - 2048 + 2^-14 in f32 loses the first 2^-14 against 2048 (f32 ulp
+# there is 2^-12) and keeps the last: 2^-14 = f16 0x0400. A pairwise sum
+# (2^-14 + 2048) + (-2048 + 2^-14) would give +0.
+# No fused multiply-add: alpha = 1 + 2^-23, a = b = 1 + 2^-10 (f16) / 1 + 2^-7 (bf16).
+# t = alpha*a rounds to 1 + 2^-10 + 2^-23 (the 2^-33 term drops), t*b rounds again, so the
+# second term -t*b cancels the first exactly: +0. A fused acc + t*(-b) would keep the
+# dropped -2^-33 (f16: -0, 0x8000) or -2^-30 (bf16: 0xB080).
+ALPHA_1ULP = float(np.float32(1.0 + 2.0 ** -23))
+GEMM_16_ORDER_KATS = [
+    ("f16", [2.0 ** -14, 2048.0, -2048.0, 2.0 ** -14], [1.0] * 4, [0.0], 1.0, 0.0, 0x0400),
+    ("f16", [1.0 + 2.0 ** -10] * 2, [1.0 + 2.0 ** -10, -1.0 - 2.0 ** -10], [0.0], ALPHA_1ULP, 0.0,
+     0x0000),
+    ("bf16", [1.0 + 2.0 ** -7] * 2, [1.0 + 2.0 ** -7, -1.0 - 2.0 ** -7], [0.0], ALPHA_1ULP, 0.0,
+     0x0000),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_16_ORDER_KATS)
+def test_gemm_seq_16_keeps_k_order_and_rounds_each_multiply(case):
+    test_gemm_seq_16_on_the_reference_known_answers(case)
+
+
+def test_the_fused_results_the_order_cases_rule_out():
+    from fractions import Fraction as F
+    for e, want in ((2.0 ** -10, -(F(2) ** -33)), (2.0 ** -7, -(F(2) ** -30))):
+        t = np.float32(ALPHA_1ULP) * np.float32(1.0 + e)
+        p = t * np.float32(1.0 + e)
+        assert F(float(p)) - F(float(t)) * F(1.0 + e) == want
+    assert int(oracle.f32_to_f16(np.array([-(2.0 ** -33)], np.float32))[0]) == 0x8000
+    assert int(oracle.f32_to_bf16(np.array([-(2.0 ** -30)], np.float32))[0]) == 0xB080
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_gemm_seq_16_matches_a_numpy_restatement_on_strided_views(kind):
+    """The C loop against an independent numpy evaluation of the same arithmetic (f32
+    elementwise products and sums, k ascending) on random data with transposed A and B,
+    bit for bit."""
+    g = np.random.default_rng(7 + (kind == "bf16"))
+    m, k, n = 23, 41, 19
+    alpha, beta = float(np.float32(1.0 / 3.0)), float(np.float32(-0.7))
+
+    def rand16(shape):
+        x = g.uniform(-2, 2, shape).astype(np.float32)
+        return oracle.f32_to_f16(x) if kind == "f16" else oracle.f32_to_bf16(x)
+    a = rand16((k, m)).T          # strides (1, m)
+    b = rand16((n, k)).T          # strides (1, k)
+    c = rand16((m, n))
+    got = oracle.gemm_seq_16(kind, alpha, beta, a, b, c)
+    widen = (lambda h: h.view(np.float16).astype(np.float32)) if kind == "f16" else oracle.bf16_to_f32
+    a32, b32 = widen(np.ascontiguousarray(a)), widen(np.ascontiguousarray(b))
+    acc = np.float32(beta) * widen(c)
+    for t in range(k):
+        acc = acc + (np.float32(alpha) * a32[:, t:t + 1]) * b32[t:t + 1, :]
+    want = acc.astype(np.float16).view(np.uint16) if kind == "f16" else oracle.f32_to_bf16(acc)
+    assert np.array_equal(got, want)
