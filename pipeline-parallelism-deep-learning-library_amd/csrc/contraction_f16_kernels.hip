@@ -58,63 +58,10 @@ __device__ inline uint16_t d2h(double x) {
     return static_cast<uint16_t>(sign | static_cast<uint32_t>(kept));
 }
 
-// bf16 bits -> double, exact (a bf16 is the high half of an f32).
-__device__ inline double b2d(uint16_t bits) {
-    return static_cast<double>(__builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16));
-}
-
-// f64 -> bf16 bits, round to nearest even, with bf16 subnormals, overflow to infinity and NaN
-// as the quiet NaN of the same sign; integer arithmetic on the f64 fields, one rounding.
-__device__ inline uint16_t d2b(double x) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, x);
-    const uint32_t sign = static_cast<uint32_t>(b >> 48) & 0x8000u;
-    const uint64_t rest = b & 0x7fffffffffffffffull;
-    if (rest > 0x7ff0000000000000ull) return static_cast<uint16_t>(sign | 0x7fc0u);
-    if (rest == 0x7ff0000000000000ull) return static_cast<uint16_t>(sign | 0x7f80u);
-    const int e = static_cast<int>(rest >> 52) - 1023;
-    const uint64_t mant = rest & 0xfffffffffffffull;
-    if (e > 127) return static_cast<uint16_t>(sign | 0x7f80u);
-    if (e >= -126) {
-        uint32_t exp8 = static_cast<uint32_t>(e + 127);
-        uint64_t kept = mant >> 45;
-        const uint64_t dropped = mant & ((1ull << 45) - 1);
-        const uint64_t halfway = 1ull << 44;
-        if (dropped > halfway || (dropped == halfway && (kept & 1))) {
-            if (++kept == 0x80) {
-                kept = 0;
-                if (++exp8 >= 255) return static_cast<uint16_t>(sign | 0x7f80u);
-            }
-        }
-        return static_cast<uint16_t>(sign | (exp8 << 7) | static_cast<uint32_t>(kept));
-    }
-    if (e < -134) return static_cast<uint16_t>(sign);  // below half the smallest subnormal
-    // Subnormal bf16: units of 2^-133. x = sig * 2^(e-52) with the implicit bit at 52.
-    const uint64_t sig = mant | (1ull << 52);
-    const int shift = -81 - e;  // 46 .. 53
-    uint64_t kept = sig >> shift;
-    const uint64_t dropped = sig & ((1ull << shift) - 1);
-    const uint64_t halfway = 1ull << (shift - 1);
-    if (dropped > halfway || (dropped == halfway && (kept & 1))) ++kept;  // 0x80 = min normal
-    return static_cast<uint16_t>(sign | static_cast<uint32_t>(kept));
-}
-
-// HK selects the 16-bit type: 0 = f16, 1 = bf16 (the Backend gemm's second 16-bit dtype).
-template <int HK>
-__device__ inline double widen(uint16_t bits) {
-    if constexpr (HK == 1) return b2d(bits);
-    else return h2d(bits);
-}
-template <int HK>
-__device__ inline uint16_t narrow(double x) {
-    if constexpr (HK == 1) return d2b(x);
-    else return d2h(x);
-}
-
-template <int HK>
 __device__ inline uint16_t finish(double acc, float alpha, float beta, const uint16_t* c) {
     double r = acc * static_cast<double>(alpha);
-    if (beta != 0.0f) r = r + static_cast<double>(beta) * widen<HK>(*c);
-    return narrow<HK>(r);
+    if (beta != 0.0f) r = r + static_cast<double>(beta) * h2d(*c);
+    return d2h(r);
 }
 
 // 64x64 output tile per 256-thread workgroup: 4 waves in 2x2, each 32x32 = 2x2 blocks of
@@ -180,29 +127,23 @@ __device__ inline void hstage(uint16_t* __restrict__ st, const h8 (&r)[HCH], int
     }
 }
 
-// Element (row, k) of a stage, widened exactly to f64.
-template <int MODE, int HK>
-__device__ inline double hval(const uint16_t* __restrict__ st, int row, int k) {
-    return widen<HK>(MODE == LOAD_MN ? st[k * HP + row] : st[row * HP + k]);
-}
-
 // Elements (row, k0 .. k0+3) of a stage, widened exactly: one 64-bit LDS read from a
 // [row][k] stage (k0 is a multiple of four, rows are 144 bytes), four 16-bit reads from a
 // [k][row] one.
-template <int MODE, int HK>
+template <int MODE>
 __device__ inline void hval4(double (&v)[4], const uint16_t* __restrict__ st, int row, int k0) {
     if constexpr (MODE == LOAD_MN) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = widen<HK>(st[(k0 + j) * HP + row]);
+        for (int j = 0; j < 4; ++j) v[j] = h2d(st[(k0 + j) * HP + row]);
     } else {
         typedef uint16_t h4 __attribute__((ext_vector_type(4)));
         const h4 w = *reinterpret_cast<const h4*>(st + row * HP + k0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = widen<HK>(w[j]);
+        for (int j = 0; j < 4; ++j) v[j] = h2d(w[j]);
     }
 }
 
-template <int AM, int BMD, int HK>
+template <int AM, int BMD>
 __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[4 * H_STAGE];
     uint16_t* As = smem;
@@ -253,9 +194,9 @@ __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
         for (int q = 0; q < HGEMM_BK / 16; ++q) {
             double av[2][4], bv[2][4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) hval4<AM, HK>(av[i], as, wm * 32 + i * 16 + li, q * 16 + lk * 4);
+            for (int i = 0; i < 2; ++i) hval4<AM>(av[i], as, wm * 32 + i * 16 + li, q * 16 + lk * 4);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) hval4<BMD, HK>(bv[j], bs, wn * 32 + j * 16 + li, q * 16 + lk * 4);
+            for (int j = 0; j < 2; ++j) hval4<BMD>(bv[j], bs, wn * 32 + j * 16 + li, q * 16 + lk * 4);
 #pragma unroll
             for (int st = 0; st < 4; ++st)
 #pragma unroll
@@ -282,7 +223,7 @@ __global__ __launch_bounds__(HT, 4) void gemm_f16_f64mfma(GemmHalfArgs p) {
                 const uint32_t col = n0 + wn * 32 + j * 16 + li;
                 if (inner || (row < p.m && col < p.n)) {
                     uint16_t* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
-                    *q = finish<HK>(acc[i][j][v], p.alpha, p.beta, q);
+                    *q = finish(acc[i][j][v], p.alpha, p.beta, q);
                 }
             }
 }
@@ -299,7 +240,6 @@ __device__ inline int64_t decode4(const Axes4& ax, uint64_t idx) {
 }
 
 // Groups that keep several strides after merging: one thread per output, K in order.
-template <int HK>
 __global__ __launch_bounds__(256) void general_f16(GeneralHalfArgs p) {
     const uint64_t mn = static_cast<uint64_t>(p.m) * p.n;
     const uint64_t count = mn * p.batch;
@@ -313,7 +253,7 @@ __global__ __launch_bounds__(256) void general_f16(GeneralHalfArgs p) {
         uint32_t dig[4] = {0, 0, 0, 0};
         int64_t oa = 0, ob = 0;
         for (uint32_t kk = 0; kk < p.k; ++kk) {
-            acc = acc + widen<HK>(a[oa]) * widen<HK>(b[ob]);
+            acc = acc + h2d(a[oa]) * h2d(b[ob]);
 #pragma unroll
             for (int d = 3; d >= 0; --d) {
                 oa += p.a_k.stride[d];
@@ -325,12 +265,11 @@ __global__ __launch_bounds__(256) void general_f16(GeneralHalfArgs p) {
             }
         }
         uint16_t* q = p.c + decode4(p.c_batch, bi) + decode4(p.c_m, mi) + decode4(p.c_n, ni);
-        *q = finish<HK>(acc, p.alpha, p.beta, q);
+        *q = finish(acc, p.alpha, p.beta, q);
     }
 }
 
 // C = 0 without reading C, or C = beta*C rounded once (the product is exact in f64).
-template <int HK>
 __global__ __launch_bounds__(256) void fill_f16(FillHalfArgs p) {
     const uint64_t mn = static_cast<uint64_t>(p.m) * p.n;
     for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < p.count;
@@ -339,7 +278,7 @@ __global__ __launch_bounds__(256) void fill_f16(FillHalfArgs p) {
         const uint64_t mi = rem / p.n, ni = rem - mi * p.n;
         uint16_t* q = p.c + decode4(p.c_batch, bi) + decode4(p.c_m, mi) + decode4(p.c_n, ni);
         *q = p.beta == 0.0f ? static_cast<uint16_t>(0)
-                            : narrow<HK>(static_cast<double>(p.beta) * widen<HK>(*q));
+                            : d2h(static_cast<double>(p.beta) * h2d(*q));
     }
 }
 
@@ -357,13 +296,9 @@ uint64_t gemm_half_workgroups(uint32_t m, uint32_t n, uint32_t batch) {
 void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int a_mode,
                       int b_mode) {
     const dim3 grid(static_cast<uint32_t>(gemm_half_workgroups(args.m, args.n, args.batch)));
-#define LG_HGEMM_CASE(AMV, BMV)                                                              \
-    if (a_mode == AMV && b_mode == BMV) {                                                    \
-        if (args.kind == 1) {                                                                \
-            hipLaunchKernelGGL((gemm_f16_f64mfma<AMV, BMV, 1>), grid, dim3(HT), 0, s, args); \
-        } else {                                                                             \
-            hipLaunchKernelGGL((gemm_f16_f64mfma<AMV, BMV, 0>), grid, dim3(HT), 0, s, args); \
-        }                                                                                    \
+#define LG_HGEMM_CASE(AMV, BMV)                                                       \
+    if (a_mode == AMV && b_mode == BMV) {                                             \
+        hipLaunchKernelGGL((gemm_f16_f64mfma<AMV, BMV>), grid, dim3(HT), 0, s, args); \
     } else
     LG_HGEMM_CASE(LOAD_K, LOAD_K)
     LG_HGEMM_CASE(LOAD_K, LOAD_MN)
@@ -376,29 +311,20 @@ void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int
     LG_HGEMM_CASE(LOAD_S, LOAD_S) { fail_invalid("unknown operand load mode"); }
 #undef LG_HGEMM_CASE
     check_hip(hipGetLastError(), "gemm_f16_f64mfma");
-    note_launch(ctx, args.kind == 1 ? "gemm_bf16_f64mfma" : "gemm_f16_f64mfma");
+    note_launch(ctx, "gemm_f16_f64mfma");
 }
 
 void launch_general_half(Context* ctx, hipStream_t s, const GeneralHalfArgs& args) {
     const uint64_t count = static_cast<uint64_t>(args.m) * args.n * args.batch;
-    if (args.kind == 1) {
-        hipLaunchKernelGGL(general_f16<1>, dim3(grid_for(count)), dim3(256), 0, s, args);
-    } else {
-        hipLaunchKernelGGL(general_f16<0>, dim3(grid_for(count)), dim3(256), 0, s, args);
-    }
+    hipLaunchKernelGGL(general_f16, dim3(grid_for(count)), dim3(256), 0, s, args);
     check_hip(hipGetLastError(), "general_f16");
-    note_launch(ctx, args.kind == 1 ? "general_bf16" : "general_f16");
+    note_launch(ctx, "general_f16");
 }
 
 void launch_fill_half(Context* ctx, hipStream_t s, const FillHalfArgs& args) {
-    if (args.kind == 1) {
-        hipLaunchKernelGGL(fill_f16<1>, dim3(grid_for(args.count)), dim3(256), 0, s, args);
-    } else {
-        hipLaunchKernelGGL(fill_f16<0>, dim3(grid_for(args.count)), dim3(256), 0, s, args);
-    }
+    hipLaunchKernelGGL(fill_f16, dim3(grid_for(args.count)), dim3(256), 0, s, args);
     check_hip(hipGetLastError(), "fill_f16");
-    if (args.kind == 1) note_launch(ctx, args.beta == 0.0f ? "zero_bf16" : "scale_bf16");
-    else note_launch(ctx, args.beta == 0.0f ? "zero_f16" : "scale_f16");
+    note_launch(ctx, args.beta == 0.0f ? "zero_f16" : "scale_f16");
 }
 
 }  // namespace lg

@@ -247,7 +247,6 @@ struct GemmHalfArgs {
     int64_t a_sb, a_sm, a_sk, b_sb, b_sn, b_sk, c_sb, c_sm, c_sn;
     uint32_t m, n, k, batch, tiles_m, tiles_n;
     float alpha, beta;
-    uint32_t kind;  // 16-bit element type: 0 = f16, 1 = bf16
 };
 struct GeneralHalfArgs {
     const uint16_t* a;
@@ -256,7 +255,6 @@ struct GeneralHalfArgs {
     uint32_t m, n, k, batch;
     float alpha, beta;
     Axes4 a_batch, a_m, a_k, b_batch, b_n, b_k, c_batch, c_m, c_n;
-    uint32_t kind;
 };
 struct FillHalfArgs {
     uint16_t* c;
@@ -264,7 +262,6 @@ struct FillHalfArgs {
     uint32_t m, n, batch;
     float beta;
     Axes4 c_batch, c_m, c_n;
-    uint32_t kind;
 };
 // The Backend's 16-bit gemm with CpuBackend's f32 arithmetic (one lane per output, k in
 // order, one rounding per multiply and add, one 16-bit rounding at the end). Operands are 2-D
