@@ -398,8 +398,9 @@ static void enqueue_gemm16(lg_ctx* ctx, hipStream_t s, const lg_tensor* a, const
     g.m = static_cast<uint32_t>(m);
     g.n = static_cast<uint32_t>(n);
     g.k = static_cast<uint32_t>(k);
-    g.tiles_m = (g.m + GEMM16_SEQ_TILE - 1) / GEMM16_SEQ_TILE;
-    g.tiles_n = (g.n + GEMM16_SEQ_TILE - 1) / GEMM16_SEQ_TILE;
+    g.tile = gemm16_seq_workgroups(g.m, g.n, GEMM16_SEQ_TILE) < 2 * GEMM16_SEQ_CUS ? 64 : GEMM16_SEQ_TILE;
+    g.tiles_m = (g.m + g.tile - 1) / g.tile;
+    g.tiles_n = (g.n + g.tile - 1) / g.tile;
     g.alpha = alpha;
     g.beta = beta;
     g.kind = a->dtype == LG_DTYPE_BF16 ? 1 : 0;

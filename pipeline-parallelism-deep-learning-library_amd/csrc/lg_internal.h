@@ -275,10 +275,13 @@ struct Gemm16SeqArgs {
     float alpha, beta;
     uint32_t kind;  // 0 = f16, 1 = bf16
     uint32_t a_kfast, b_kfast;
+    uint32_t tile;  // square output tile: 128, or 64 where 128x128 tiles would not fill two
+                    // workgroups per compute unit (fewer than 2 * GEMM16_SEQ_CUS tiles)
 };
-constexpr uint32_t GEMM16_SEQ_TILE = 128;  // square output tile of the kernel
+constexpr uint32_t GEMM16_SEQ_TILE = 128;
+constexpr uint32_t GEMM16_SEQ_CUS = 256;  // compute units of the part
 void launch_gemm16_seq(Context* ctx, hipStream_t s, const Gemm16SeqArgs& args);
-uint64_t gemm16_seq_workgroups(uint32_t m, uint32_t n);
+uint64_t gemm16_seq_workgroups(uint32_t m, uint32_t n, uint32_t tile);
 
 void launch_gemm_half(Context* ctx, hipStream_t s, const GemmHalfArgs& args, int a_mode,
                       int b_mode);

@@ -417,9 +417,11 @@ ALPHA_THIRD = float(np.float32(1.0 / 3.0))
 @pytest.mark.parametrize("layout", ["rm", "at", "bt"])
 @pytest.mark.parametrize("m,k,n,alpha,beta", [(64, 64, 64, 1.0, 0.0), (130, 300, 70, 0.75, -0.5),
                                               (256, 512, 192, ALPHA_THIRD, 0.7), (3, 1000, 5, -2.0, 0.0),
-                                              (129, 17, 257, ALPHA_THIRD, 1.0), (1, 1, 1, 1.5, 0.5)])
+                                              (129, 17, 257, ALPHA_THIRD, 1.0), (1, 1, 1, 1.5, 0.5),
+                                              (4096, 24, 2000, ALPHA_THIRD, 0.7)])
 def test_16_bit_gemm_is_bit_exact_with_the_cpu_restatement(hb, kind, layout, m, k, n, alpha, beta):
-    """Random data, every supported layout, ragged tiles and K slices: the device repeats
+    """Random data, every supported layout, ragged tiles and K slices, on 64x64 tiles (grids
+    of fewer than 512 128x128 tiles) and 128x128 ones (the 4096 x 2000 output): the device repeats
     CpuBackend's f32 arithmetic per output (beta*C, then (alpha*a)*b added in k order, each
     step rounded, one 16-bit rounding at the end), so every output has the oracle's bits."""
     g = rng(m * 31 + k * 7 + n + (kind == "bf16") + 3 * len(layout))
