@@ -35,6 +35,9 @@ METRIC = "contraction TFLOP/s (% fp32 MFMA peak); permute GB/s (% HBM peak)"
 PEAK_TFLOPS = 157.3     # MI355X dense fp32 MFMA
 PEAK_GBS = 8000.0       # MI355X HBM3E
 PEAK_F64_TFLOPS = 78.6  # MI355X dense fp64 MFMA
+# Non-packed f32 VALU operations: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz = 39.3e12 per second;
+# the 16-bit Backend gemm spends two (one multiply, one add) per term.
+PEAK_VALU_TOPS = 39.3
 
 
 class HipEvents:
@@ -432,6 +435,36 @@ def bench_gemm_f16(ctx, events, pool, L, C, m, n, k, args):
     return res
 
 
+def bench_backend_gemm16(events, args, timed_fn, m=4096, n=4096, k=4096):
+    """Backend::gemm on F16 tensors, bit-exact with CpuBackend (one lane per output runs the
+    reference's serial f32 chain): 10^12 terms (multiply-add pairs) per second against the VALU
+    bound of two f32 operations per term."""
+    import oracle
+    from linalg_hip import backend as B
+    hb = B.HipBackend(0)
+    g = np.random.Generator(np.random.PCG64(37))
+    a16 = oracle.f32_to_f16(g.uniform(-1, 1, m * k).astype(np.float32))
+    b16 = oracle.f32_to_f16(g.uniform(-1, 1, k * n).astype(np.float32))
+    ta = hb.upload(B.DType.F16, [m, k], a16.tobytes())
+    tb = hb.upload(B.DType.F16, [k, n], b16.tobytes())
+    tc = hb.alloc(B.DType.F16, [m, n])
+    ms = timed_fn(hb.ctx, events, lambda: hb.gemm(ta, tb, tc, 1.0, 0.0), args.steps, args.warmup)
+    terms = m * n * k / (ms * 1e-3) / 1e12
+    res = {"name": f"Backend::gemm f16 {m}x{n}x{k} (CpuBackend's f32 chain, bit-exact)", "ms": ms,
+           "tterms": terms, "frac_valu": 2 * terms / PEAK_VALU_TOPS, "kernel": "gemm16_seq<0, 8>"}
+    hb.close()
+    if not args.no_cpu:
+        rows = 4
+        out = np.zeros((rows, n), np.uint16)
+        t0 = time.perf_counter()
+        oracle.gemm_seq_16("f16", 1.0, 0.0, a16.reshape(m, k)[:rows], b16.reshape(k, n), out)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(rows * n * k / dt / 1e12, 6), "unit": "10^12 terms/s",
+                               "cores": 1, "kind": "port",
+                               "sample": f"{rows} of {m} output rows, CpuBackend's loop ({dt:.2f} s)"}
+    return res
+
+
 def bench_train_ops(events, args, timed_fn):
     """The Backend activation and training ops at the config-5 layer shape [4096, 16384]
     (Y = X.W of the 1F1B linear step): each op's algorithmic bytes / mean kernel time."""
@@ -713,8 +746,8 @@ def main() -> int:
                          "clock); 0 turns it off")
     ap.add_argument("--only", default=None,
                     help="run only these workloads (comma-separated): gemm4096, sq1024, sq2048, c1, c3, c4, c5, c2a, c2b, c2b_1g, copy, t8191, floor, "
-                         "train, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, o_rank4, "
-                         "o_f16_2048")
+                         "train, bgemm16, f16, o_t2048, o_batched, o_dot, o_32k1m, o_rank1, "
+                         "o_rank4, o_f16_2048")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--vendor", action="store_true",
                     help="also time the vendor library on the square GEMMs and config 3, as the "
@@ -840,6 +873,7 @@ def main() -> int:
                 "ms_graph": graph_rate(ctx, events, launch, args.steps), "kernels": kernels}
     run("floor", floor)
     run("train", lambda: bench_train_ops(events, args, timed))
+    run("bgemm16", lambda: bench_backend_gemm16(events, args, timed))
     run("f16", lambda: bench_gemm_f16(ctx, events, pool, L, C, 4096, 4096, 4096, args))
     # The reference's own benchmark list (tests/contraction_test.rs:1293-1395).
     for key, name, a_spec, b_spec, c_spec in other_paths_specs():
@@ -850,6 +884,7 @@ def main() -> int:
         print("[bench] vendor ...", file=sys.stderr, flush=True)
         attach_vendor(results, args)
     train = results.pop("train", None)
+    bgemm16 = results.pop("bgemm16", None)
     if not args.no_cpu:
         print("[bench] cpu baselines ...", file=sys.stderr, flush=True)
         attach_cpu_baselines(results, min(os.cpu_count() or 1, 16))
@@ -904,6 +939,18 @@ def main() -> int:
                          "kernel": "gemm_f16_f64mfma<0, 1> (v_mfma_f64_16x16x4_f64)",
                          "profile": "profiles/gemm_f16_f64mfma_4096.md"},
             "cpu_baseline": f16.get("cpu_baseline")}
+    if bgemm16:
+        line["backend_gemm16"] = {
+            "value": round(bgemm16["tterms"], 3), "unit": "10^12 terms/s",
+            "workload": bgemm16["name"], "ms_per_step": round(bgemm16["ms"], 4),
+            "roofline": {"bound": "valu", "achieved": round(2 * bgemm16["tterms"], 3),
+                         "peak": PEAK_VALU_TOPS, "unit": "10^12 f32 ops/s",
+                         "frac": round(bgemm16["frac_valu"], 4), "kernel": bgemm16["kernel"],
+                         "peak_model": "one wave64 f32 VALU instruction per SIMD per 4 cycles "
+                                       "(1024 SIMDs x 16 lanes x 2.4 GHz); the kernel's counters "
+                                       "show 0.306 per SIMD per cycle, above this model",
+                         "profile": "profiles/gemm16_seq_backend4096.md"},
+            "cpu_baseline": bgemm16.get("cpu_baseline")}
     if train:
         shape = train.pop("_shape")
         line["train_ops"] = {
