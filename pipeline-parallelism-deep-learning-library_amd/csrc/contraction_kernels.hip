@@ -191,11 +191,23 @@ __global__ __launch_bounds__(OUTER_THREADS) void outer_f32(GemmArgs p) {
     const uint32_t nq = (p.n + 3) / 4;
     const uint64_t total = static_cast<uint64_t>(p.batch) * p.m * nq;
     const float alpha_a = p.scale_b ? 1.0f : p.alpha, alpha_b = p.scale_b ? p.alpha : 1.0f;
+    // Index arithmetic in 32 bits when every output quad's index fits (the 64-bit divisions
+    // otherwise cost more VALU time than the thread's 16 bytes of stores).
+    const bool narrow = total <= 0xffffffffull;
     for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * OUTER_THREADS + threadIdx.x; t < total;
          t += static_cast<uint64_t>(gridDim.x) * OUTER_THREADS) {
-        const uint64_t row = t / nq;
-        const uint32_t j0 = static_cast<uint32_t>(t - row * nq) * 4;
-        const uint32_t bi = static_cast<uint32_t>(row / p.m), i = static_cast<uint32_t>(row - static_cast<uint64_t>(bi) * p.m);
+        uint32_t j0, bi, i;
+        if (narrow) {
+            const uint32_t t32 = static_cast<uint32_t>(t), row32 = t32 / nq;
+            j0 = (t32 - row32 * nq) * 4;
+            bi = p.batch == 1 ? 0u : row32 / p.m;
+            i = row32 - bi * p.m;
+        } else {
+            const uint64_t row = t / nq;
+            j0 = static_cast<uint32_t>(t - row * nq) * 4;
+            bi = static_cast<uint32_t>(row / p.m);
+            i = static_cast<uint32_t>(row - static_cast<uint64_t>(bi) * p.m);
+        }
         const uint32_t cnt = min(4u, p.n - j0);
         const float* a = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(i) * p.a_sm;
         const float* b = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(j0) * p.b_sn;
