@@ -1,11 +1,13 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X contraction / permutation hot path.
 
-Prints ONE JSON line. The headline (`value`) is fp32 contraction TFLOP/s on the north-star
-workload, C[4096,4096] = A[4096,4096] . B[4096,4096] row-major (a "step" is one such
-contraction over resident HBM inputs). The same line carries the permutation headline
-(GB/s on the 1 GiB-traffic [512,1024,256] perm (2,0,1) materialization) and every
-benchmark configuration, each with its roofline fraction:
+Prints ONE compact JSON line last on stdout (under 4000 bytes). The headline (`value`) is
+fp32 contraction TFLOP/s on the north-star workload, C[4096,4096] = A[4096,4096] .
+B[4096,4096] row-major (a "step" is one such contraction over resident HBM inputs). The same
+line carries the permutation headline (GB/s on the 1 GiB-traffic [512,1024,256] perm (2,0,1)
+materialization) and a [value, unit, roofline frac] summary of every benchmark configuration;
+each workload's full record (plan, kernels, median/best, CPU baselines) goes to the --detail
+file. Rooflines:
   contraction: achieved = 2*B*M*N*K / mean kernel time, peak = 157.3 TFLOP/s fp32 MFMA
   permutation: achieved = 2*numel*4 B / mean kernel time,  peak = 8000 GB/s HBM
 Kernel time is measured with HIP events recorded on the stream the kernels are launched on,
@@ -14,6 +16,7 @@ of untimed launches, so short kernels reach the steady clock), with the stream s
 on both sides. The CPU baseline times the C restatement of crates/cpu on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+                       [--detail FILE]
 """
 from __future__ import annotations
 
@@ -35,9 +38,9 @@ METRIC = "contraction TFLOP/s (% fp32 MFMA peak); permute GB/s (% HBM peak)"
 PEAK_TFLOPS = 157.3     # MI355X dense fp32 MFMA
 PEAK_GBS = 8000.0       # MI355X HBM3E
 PEAK_F64_TFLOPS = 78.6  # MI355X dense fp64 MFMA
-# Non-packed f32 VALU operations: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz = 39.3e12 per second;
-# the 16-bit Backend gemm spends two (one multiply, one add) per term.
-PEAK_VALU_TOPS = 39.3
+# MI355X published fp32 vector peak. The 16-bit Backend gemm spends two f32 operations (one
+# multiply, one add, never fused) per term; it is priced against this figure.
+PEAK_VECTOR_TFLOPS = 157.3
 
 
 class HipEvents:
@@ -437,8 +440,9 @@ def bench_gemm_f16(ctx, events, pool, L, C, m, n, k, args):
 
 def bench_backend_gemm16(events, args, timed_fn, m=4096, n=4096, k=4096):
     """Backend::gemm on F16 tensors, bit-exact with CpuBackend (one lane per output runs the
-    reference's serial f32 chain): 10^12 terms (multiply-add pairs) per second against the VALU
-    bound of two f32 operations per term."""
+    reference's serial f32 chain): 10^12 terms (multiply-add pairs) per second, and the two f32
+    operations per term against the published 157.3 TFLOP/s fp32 vector peak (which counts
+    packed FMA; the chain can use neither packing nor fusion)."""
     import oracle
     from linalg_hip import backend as B
     hb = B.HipBackend(0)
@@ -451,7 +455,8 @@ def bench_backend_gemm16(events, args, timed_fn, m=4096, n=4096, k=4096):
     ms = timed_fn(hb.ctx, events, lambda: hb.gemm(ta, tb, tc, 1.0, 0.0), args.steps, args.warmup)
     terms = m * n * k / (ms * 1e-3) / 1e12
     res = {"name": f"Backend::gemm f16 {m}x{n}x{k} (CpuBackend's f32 chain, bit-exact)", "ms": ms,
-           "tterms": terms, "frac_valu": 2 * terms / PEAK_VALU_TOPS, "kernel": "gemm16_seq<0, 8>"}
+           "tterms": terms, "tflops_vector": 2 * terms, "frac_vector": 2 * terms / PEAK_VECTOR_TFLOPS,
+           "kernel": "gemm16_seq<0, 8>"}
     hb.close()
     if not args.no_cpu:
         rows = 4
@@ -731,6 +736,110 @@ def attach_cpu_baselines(results, threads):
                                                  f"{threads} contiguous output ranges", threads)
 
 
+LINE_LIMIT = 4000  # bytes of the final stdout line: the driver keeps only the tail of stdout
+
+# Workloads summarised on the final line, in this order: {name: [value, unit, roofline frac]}.
+SUMMARY_ORDER = ("gemm4096", "sq1024", "sq2048", "c1", "c3", "c4", "c5", "c2a", "c2b", "c2b_1g",
+                 "copy", "t8191", "floor", "f16", "o_t2048", "o_batched", "o_dot", "o_32k1m",
+                 "o_rank1", "o_rank4", "o_f16_2048")
+
+
+def _r(x, nd=4):
+    return round(x, nd) if isinstance(x, float) else x
+
+
+def summary_entry(r):
+    """[value, unit, frac] of one workload's result: the figure its roofline is priced in."""
+    if "roofline" in r:
+        roof = r["roofline"]
+        return [_r(roof["achieved"], 2), roof["unit"], _r(roof["frac"])]
+    if "frac_f64_mfma" in r:
+        return [_r(r["tflops"], 2), "TFLOP/s f64-MFMA", _r(r["frac_f64_mfma"])]
+    if "tflops" in r:
+        return [_r(r["tflops"], 2), "TFLOP/s", _r(r["frac"])]
+    if "gbs" in r:
+        return [_r(r["gbs"], 1), "GB/s", _r(r.get("frac", r["gbs"] / PEAK_GBS))]
+    if "ms" in r:
+        return [_r(r["ms"] * 1e3, 2), "us", None]
+    return None
+
+
+def short_cpu(cb):
+    return None if not cb else {k: _r(v, 6) for k, v in cb.items()}
+
+
+def detail_record(results, args, train, bgemm16):
+    """Every workload's full result (plan, kernels, per-launch median and best, graph-replay
+    figures, CPU baselines): written to the --detail file, not to stdout."""
+    rec = {"metric": METRIC, "steps": args.steps, "warmup": args.warmup,
+           "warmup_min_ms": args.warmup_ms}
+    rec["configs"] = {k_: {kk: _r(v) for kk, v in r.items()} for k_, r in results.items()}
+    if train:
+        rec["train_ops"] = {k_: ({kk: _r(v) for kk, v in r.items()} if isinstance(r, dict) else r)
+                            for k_, r in train.items()}
+    if bgemm16:
+        rec["backend_gemm16"] = {k_: _r(v) for k_, v in bgemm16.items()}
+    if not args.no_cpu:
+        rec["cpu_host"] = host_cpu()
+    return rec
+
+
+def headline_line(results, args, train, bgemm16, detail_path):
+    """The one JSON line printed last on stdout (under LINE_LIMIT bytes): the 4096^3 headline
+    with its roofline and CPU baselines, the permutation headline, and a [value, unit, frac]
+    summary of every other workload."""
+    head = results.get("gemm4096")
+    perm = results.get("c2b")
+    line = {"metric": METRIC, "value": round(head["tflops"], 3) if head else None,
+            "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(head["ms"], 4) if head else None, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "fp32 contraction C[4096,4096] = A.B row-major (4096^3)",
+                       "m": 4096, "n": 4096, "k": 4096, "parallelism": "single-gpu"}}
+    if head:
+        line["roofline"] = {"bound": "mfma", "achieved": round(head["tflops"], 3),
+                            "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(head["frac"], 4),
+                            "traffic": traffic_from_profile("gemm4096"),
+                            "kernel": ", ".join(head.get("kernels", [])),
+                            "algorithmic": "2*4096^3 FLOP per launch"}
+        line["cpu_baseline"] = short_cpu(head.get("cpu_baseline"))
+        line["cpu_baseline_parallel"] = short_cpu(head.get("cpu_baseline_parallel"))
+    if perm:
+        line["permute"] = {"value": round(perm["gbs"], 1), "unit": "GB/s",
+                           "workload": "[512,1024,256] perm (2,0,1) materialize",
+                           "ms_per_step": round(perm["ms"], 4),
+                           "roofline": {"bound": "hbm", "achieved": round(perm["gbs"], 1),
+                                        "peak": PEAK_GBS, "unit": "GB/s",
+                                        "frac": round(perm["frac"], 4),
+                                        "traffic": traffic_from_profile("c2b"),
+                                        "kernel": ", ".join(perm.get("kernels", []))},
+                           "cpu_baseline": short_cpu(perm.get("cpu_baseline")),
+                           "cpu_baseline_parallel": short_cpu(perm.get("cpu_baseline_parallel"))}
+    summ = {}
+    for name in SUMMARY_ORDER:
+        r = results.get(name)
+        e = summary_entry(r) if isinstance(r, dict) else None
+        if e is not None:
+            summ[name] = e
+    if bgemm16:
+        summ["bgemm16"] = [_r(2 * bgemm16["tterms"], 2), "TFLOP/s f32 vector",
+                           _r(2 * bgemm16["tterms"] / PEAK_VECTOR_TFLOPS)]
+    if train:
+        for op, r in train.items():
+            if isinstance(r, dict) and "gbs" in r:
+                summ[op] = [_r(r["gbs"], 1), "GB/s", _r(r["frac"])]
+    line["configs_summary"] = summ
+    if detail_path:
+        line["detail"] = str(detail_path)
+    # Dropping optional parts keeps the line parseable whatever the workload set.
+    for key in ("detail", "cpu_baseline_parallel", "configs_summary"):
+        if len(json.dumps(line)) <= LINE_LIMIT:
+            break
+        line.pop(key, None)
+    return line
+
+
 def main() -> int:
     global WARMUP_MS
     ap = argparse.ArgumentParser()
@@ -756,6 +865,9 @@ def main() -> int:
     ap.add_argument("--prewarm", type=float, default=0.0,
                     help="seconds of 4096^3 GEMMs to run before any timing, so workloads timed "
                          "alone start at the steady shader clock")
+    ap.add_argument("--detail", default=str(Path("gpurun_out") / "bench_detail.json"),
+                    help="file for every workload's full result (the stdout line carries the "
+                         "headline and a summary); empty to skip")
     args = ap.parse_args()
     WARMUP_MS = args.warmup_ms
     if args.gpus != 1:
@@ -806,6 +918,10 @@ def main() -> int:
             print(f"[bench] {name} ...", file=sys.stderr, flush=True)
             results[name] = fn()
             pool.free()
+            r = results[name]
+            e = summary_entry(r) if isinstance(r, dict) else None
+            if e is not None:
+                print(f"[bench] {name}: {e[0]} {e[1]} (frac {e[2]})", file=sys.stderr, flush=True)
 
     run("gemm4096", lambda: bench_gemm(ctx, events, pool, L, C, "gemm 4096^3", 4096, 4096, 4096, args))
     # The reference's spec benchmark squares (tests/contraction_test.rs:1246-1291).
@@ -894,76 +1010,12 @@ def main() -> int:
             p.pop("_geom", None)
             p.pop("_other", None)
 
-    head = results.get("gemm4096")
-    perm = results.get("c2b")
-    line = {"metric": METRIC, "value": round(head["tflops"], 3) if head else None,
-            "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "warmup_min_ms": args.warmup_ms,
-            "ms_per_step": round(head["ms"], 4) if head else None, "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "fp32 contraction C[4096,4096] = A.B row-major (north-star "
-                                   "4096^3); permutation headline [512,1024,256] perm (2,0,1)",
-                       "m": 4096, "n": 4096, "k": 4096, "parallelism": "single-gpu"}}
-    if head:
-        line["roofline"] = {"bound": "mfma", "achieved": round(head["tflops"], 3),
-                            "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                            "frac": round(head["frac"], 4),
-                            "traffic": traffic_from_profile("gemm4096"),
-                            "kernel": ", ".join(head.get("kernels", [])) + " (A K-contiguous, B "
-                                      "N-contiguous, %dx%d tiles)" % tuple(head["plan"]["tile"]),
-                            "profile": "profiles/gemm_f32_pl_gemm4096.md, profiles/traffic_gemm4096.txt",
-                            "algorithmic": "2*4096^3 = 137.44 GFLOP per launch"}
-    if head and "cpu_baseline" in head:
-        line["cpu_baseline"] = head["cpu_baseline"]
-        line["cpu_baseline_parallel"] = head["cpu_baseline_parallel"]
-    if perm:
-        line["permute"] = {"value": round(perm["gbs"], 1), "unit": "GB/s",
-                           "workload": perm["name"], "ms_per_step": round(perm["ms"], 4),
-                           "roofline": {"bound": "hbm", "achieved": round(perm["gbs"], 1),
-                                        "peak": PEAK_GBS, "unit": "GB/s",
-                                        "frac": round(perm["frac"], 4),
-                                        "traffic": traffic_from_profile("c2b"),
-                                        "kernel": ", ".join(perm.get("kernels", [])),
-                                        "profile": "profiles/perm_tile_c2b.md, profiles/traffic_c2b.txt",
-                                        "algorithmic": "2*134217728*4 B = 1 GiB per launch"},
-                           "cpu_baseline": perm.get("cpu_baseline"),
-                           "cpu_baseline_parallel": perm.get("cpu_baseline_parallel")}
-    f16 = results.get("f16")
-    if f16:
-        line["contract_f16"] = {
-            "value": round(f16["tflops"], 3), "unit": "TFLOP/s", "workload": f16["name"],
-            "ms_per_step": round(f16["ms"], 4),
-            "roofline": {"bound": "mfma", "achieved": round(f16["tflops"], 3),
-                         "peak": PEAK_F64_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(f16["frac_f64_mfma"], 4),
-                         "kernel": "gemm_f16_f64mfma<0, 1> (v_mfma_f64_16x16x4_f64)",
-                         "profile": "profiles/gemm_f16_f64mfma_4096.md"},
-            "cpu_baseline": f16.get("cpu_baseline")}
-    if bgemm16:
-        line["backend_gemm16"] = {
-            "value": round(bgemm16["tterms"], 3), "unit": "10^12 terms/s",
-            "workload": bgemm16["name"], "ms_per_step": round(bgemm16["ms"], 4),
-            "roofline": {"bound": "valu", "achieved": round(2 * bgemm16["tterms"], 3),
-                         "peak": PEAK_VALU_TOPS, "unit": "10^12 f32 ops/s",
-                         "frac": round(bgemm16["frac_valu"], 4), "kernel": bgemm16["kernel"],
-                         "peak_model": "one wave64 f32 VALU instruction per SIMD per 4 cycles "
-                                       "(1024 SIMDs x 16 lanes x 2.4 GHz); the kernel's counters "
-                                       "show 0.306 per SIMD per cycle, above this model",
-                         "profile": "profiles/gemm16_seq_backend4096.md"},
-            "cpu_baseline": bgemm16.get("cpu_baseline")}
-    if train:
-        shape = train.pop("_shape")
-        line["train_ops"] = {
-            "workload": f"Backend ops on f32 [{shape[0]}, {shape[1]}] (the config-5 layer "
-                        "activation), HBM roofline, algorithmic bytes = every operand read and "
-                        "written once",
-            "peak_gbs": PEAK_GBS,
-            "ops": {k_: {kk: (round(v, 4) if isinstance(v, float) else v) for kk, v in r.items()}
-                    for k_, r in train.items()}}
-    if not args.no_cpu:
-        line["cpu_host"] = host_cpu()
-    line["configs"] = {k_: {kk: (round(v, 4) if isinstance(v, float) else v)
-                            for kk, v in r.items()} for k_, r in results.items()}
+    detail = detail_record(results, args, train, bgemm16)
+    line = headline_line(results, args, train, bgemm16, args.detail)
+    if args.detail:
+        path = Path(args.detail)
+        path.parent.mkdir(parents=True, exist_ok=True)
+        path.write_text(json.dumps(detail, indent=1) + "\n")
     print(json.dumps(line), flush=True)
     ctx.close()
     return 0

@@ -25,6 +25,12 @@
  *  - Thread safety: calls on different streams may run concurrently. As in
  *    crates/core/src/lib.rs:67-70, the caller must not let two in-flight calls write
  *    overlapping memory.
+ *  - Split scratch: every split-K and split-dot plan (lg_contract_plan.scratch_bytes > 0)
+ *    of one context shares that context's one scratch buffer. Eager calls are ordered on it
+ *    by the library (stream order, or an event when the stream changes). A call recorded
+ *    under stream capture is ordered only by its own stream: replays of that graph must not
+ *    overlap one another or any other split call on the same context, whatever the stream
+ *    (the caller orders them, or gives each concurrent stream its own context).
  */
 #ifndef LINALG_HIP_H
 #define LINALG_HIP_H
@@ -166,7 +172,8 @@ lg_status lg_adjoint(lg_ctx* ctx, lg_elem elem, const lg_view* src, const lg_vie
  * three: a batch axis. beta = 0 never reads C, alpha = 0 never reads A or B, K = 0 gives
  * C = beta * C, an empty M, N or batch launches nothing. LG_OVERLAP when C aliases an input
  * it reads or writes an element twice (the in-place scale with the other extents 1 is
- * allowed). */
+ * allowed). Split plans use the context's shared scratch: under stream capture see
+ * "Split scratch" above. */
 lg_status lg_encode_contract_f32(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
                                  const char* a_labels, const lg_view* b, const char* b_labels,
                                  float beta, const lg_view* c, const char* c_labels);
@@ -177,7 +184,8 @@ lg_status lg_contract_f32(lg_ctx* ctx, float alpha, const lg_view* a, const char
 /* encode_gemm / gemm / gemm_nowait (src/ops/contraction.rs:1066-1130): batched matrix form.
  * Equal ranks r >= 2; leading r-2 axes are batch; A[..., M, K], B[..., K, N], C[..., M, N].
  * Strides may describe transposes or windows; nothing is copied. gemm_nowait enqueues on
- * the context stream and returns without waiting. */
+ * the context stream and returns without waiting. Split plans use the context's shared
+ * scratch: under stream capture see "Split scratch" above. */
 lg_status lg_encode_gemm_f32(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
                              const lg_view* b, float beta, const lg_view* c);
 lg_status lg_gemm_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view* b, float beta,

@@ -189,6 +189,7 @@ lg_status lg_ctx_create(int32_t device, lg_ctx** out) {
         std::unique_ptr<lg_ctx> ctx(new lg_ctx());
         ctx->device = device;
         for (auto& n : ctx->names) n.store(nullptr);
+        noalloc_prepare(ctx.get());  // before anything the context would have to release
         check_hip(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
         // The split partials' scratch, made once here so no enqueue ever allocates (stream
         // capture included).

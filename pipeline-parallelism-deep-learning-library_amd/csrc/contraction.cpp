@@ -608,6 +608,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     info.k = mg.k_n;
     info.splits = 1;
     info.k_chunk = mg.k_n;
+    info.kgroups = 1;
     info.groups = static_cast<uint32_t>(
         std::max({mg.batch.size(), mg.m.size(), mg.n.size(), mg.k.size()}));
     if (mg.m_n == 0 || mg.n_n == 0 || mg.batch_n == 0) {

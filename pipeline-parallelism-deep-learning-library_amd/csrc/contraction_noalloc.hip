@@ -3,10 +3,11 @@
 //
 // Its split-K and split-dot partials live in `scratch`, a file-scope device array of
 // SCRATCH_BYTES (32 MiB, the most any plan uses: the planner caps split counts to fit), which
-// each GPU holds from the library's first use on it until the process ends. In host code the
+// each GPU holds from the first context made on it until the process ends. In host code the
 // array's name is only a stand-in: its device address on each GPU is looked up once per device
-// with hipGetSymbolAddress, on the entry point's first call there, and only that address is
-// handed to kernels. Every partial is written before it is read within one call, so nothing
+// with hipGetSymbolAddress, when lg_ctx_create makes the first context there (so the code
+// object holding the array is loaded then, never under a later stream capture), and only that
+// address is handed to kernels. Every partial is written before it is read within one call, so nothing
 // needs clearing. Every call on one GPU shares that GPU's array, so calls that overlap on one
 // GPU (several streams, several contexts, or graph replays running at once) race on it: the
 // caller orders them. Nothing here allocates: no hipMalloc, no hipFree, no allocating library
@@ -43,6 +44,9 @@ float* scratch_on(lg_ctx* ctx) {
 }
 
 }  // namespace
+
+void noalloc_prepare(lg_ctx* ctx) { (void)scratch_on(ctx); }
+
 }  // namespace lg
 
 using namespace lg;

@@ -385,6 +385,9 @@ void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, 
 void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg_view* a,
                                 const lg_view* b, float beta, const lg_view* c,
                                 uint64_t partial_cap, float* (*scratch)(lg_ctx*));
+// Looks up the no-allocation entry point's static scratch on the context's device (current
+// when called), so its code object is loaded at context creation and never inside a capture.
+void noalloc_prepare(lg_ctx* ctx);
 inline hipStream_t pick_stream(const lg_ctx* ctx, void* stream) {
     return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
 }

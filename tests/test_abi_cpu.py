@@ -574,3 +574,21 @@ def test_context_without_a_device_is_no_device():
     st = N.lib().lg_ctx_create(0, ctypes.byref(ctx))
     assert st == 1 and not ctx.value  # LG_NO_DEVICE
     assert b"no HIP device" in N.lib().lg_last_error()
+
+
+def test_plans_without_a_k_split_report_one_wave_group():
+    """kgroups is 1 on every plan whose kernel does not split a tile's K among wave groups:
+    outer (K <= 8), dot, fill, general and the plain tiled kernels."""
+    cases = [
+        ((dense([4096, 1]), "mk"), (dense([1, 4096]), "kn"), (dense([4096, 4096]), "mn"), "outer"),
+        ((dense([1, 1 << 20]), "mk"), (dense([1 << 20, 1]), "kn"), (dense([1, 1]), "mn"), "dot"),
+        ((dense([64, 0]), "mk"), (dense([0, 64]), "kn"), (dense([64, 64]), "mn"), None),
+        ((view(Layout(0, [6, 5, 4], [1, 30, 6])), "mxk"), (dense([4, 7]), "kn"),
+         (dense([6, 5, 7]), "mxn"), None),
+        ((dense([300, 40]), "mk"), (dense([40, 300]), "kn"), (dense([300, 300]), "mn"), None),
+    ]
+    for a, b, c, kernel in cases:
+        p = C.plan_contract(1.0, a, b, 0.0, c)
+        assert p["kgroups"] == 1, p
+        if kernel:
+            assert p["kernel"] == kernel, p

@@ -43,3 +43,104 @@ def test_cpu_baselines_attach_to_every_gemm_and_permutation_workload():
     assert res["c5"]["parts"][2]["cpu_baseline"]["unit"] == "TFLOP/s"
     assert res["c2b"]["cpu_baseline_parallel"]["cores"] == 2
     assert "cpu_baseline" not in res["copy"]
+
+
+def _stub_results():
+    """A result set shaped like a full run's: every workload, long kernel lists and samples."""
+    cpu = {"value": 0.000207, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+           "sample": "48 of 4096 output rows, literal k-order loop (3 runs, 0.81 s)"}
+    cpu_par = dict(cpu, cores=16, sample="4096 of 4096 output rows, bit-identical "
+                                         "loop-interchanged variant on 16 threads (1.20 s)")
+    plan = {"kind": "tiled", "kernel": "pipelined", "tile": [256, 128], "a_mode": "k",
+            "b_mode": "mn", "splits": 1, "workgroups": 512}
+
+    def gemm(tf):
+        return {"name": "gemm x" * 8, "ms": 0.9661, "ms_median": 0.9662, "ms_best": 0.9601,
+                "host_ms": 0.01, "tflops": tf, "frac": tf / 157.3, "plan": plan,
+                "kernels": ["gemm_f32_pl<0, 1, 16, 4, 1>", "reduce_f32"],
+                "cpu_baseline": cpu, "cpu_baseline_parallel": cpu_par}
+
+    def perm(gbs):
+        return {"name": "perm", "ms": 0.1745, "gbs": gbs, "frac": gbs / 8000.0,
+                "plan": {"kind": "tile", "vector": True, "workgroups": 8192,
+                         "shape": [256, 524288]}, "kernels": ["perm_tile_w1_v128_stream"],
+                "cpu_baseline": dict(cpu, unit="GB/s"), "cpu_baseline_parallel": cpu_par}
+
+    def other(bound):
+        roof = ({"bound": "mfma", "achieved": 114.2, "peak": 157.3, "unit": "TFLOP/s",
+                 "frac": 0.726} if bound == "mfma" else
+                {"bound": "hbm", "achieved": 4342.3, "peak": 8000.0, "unit": "GB/s",
+                 "frac": 0.543})
+        return {"name": "other", "ms": 0.2142, "tflops": 114.2, "gbs": 297.4, "roofline": roof,
+                "plan": plan, "kernels": ["gemm_f32_pl_n64<K,MN>"], "cpu_baseline": cpu}
+
+    res = {k: gemm(140.0) for k in ("gemm4096", "sq1024", "sq2048", "c1", "c3", "c4")}
+    res["c5"] = {"name": "C5", "ms": 12.0, "tflops": 137.0, "frac": 0.87,
+                 "parts": [gemm(137.0)] * 3, "cpu_baseline": cpu, "cpu_baseline_parallel": cpu_par}
+    for k in ("c2a", "c2b", "c2b_1g"):
+        res[k] = perm(6100.0)
+    res["copy"] = {"name": "copy", "gbs": 6683.7}
+    res["t8191"] = dict(perm(5325.0), copy_gbs=6718.0, ratio_vs_copy=0.79)
+    res["floor"] = {"name": "floor", "ms": 0.0099, "ms_graph": 0.0032, "kernels": ["zero_f32"]}
+    res["f16"] = {"name": "f16", "ms": 2.24, "tflops": 61.3, "frac_f64_mfma": 0.78,
+                  "cpu_baseline": cpu}
+    res["o_f16_2048"] = dict(res["f16"])
+    for k in ("o_t2048", "o_rank4"):
+        res[k] = other("mfma")
+    for k in ("o_batched", "o_dot", "o_32k1m", "o_rank1"):
+        res[k] = other("hbm")
+    train = {op: {"ms": 0.2, "gbs": 5900.0, "frac": 0.74, "bytes": 1 << 29, "kernel": op,
+                  "cpu_baseline": dict(cpu, unit="GB/s")}
+             for op in ("gelu", "gelu_backward", "add_bias", "bias_grad", "mse_grad", "sgd_step",
+                        "convert_f32_bf16", "convert_bf16_f32")}
+    bgemm16 = {"name": "bgemm16", "ms": 3.3, "tterms": 20.7, "tflops_vector": 41.4,
+               "frac_vector": 0.263, "kernel": "gemm16_seq<0, 8>", "cpu_baseline": cpu}
+    return res, train, bgemm16
+
+
+def test_headline_line_is_compact_and_carries_the_required_keys():
+    sys.path.insert(0, str(REPO))
+    import bench
+
+    class Args:
+        steps, warmup, warmup_ms, no_cpu = 20, 50, 30.0, False
+    res, train, bgemm16 = _stub_results()
+    line = bench.headline_line(res, Args, train, bgemm16, "gpurun_out/bench_detail.json")
+    text = json.dumps(line)
+    assert len(text) <= bench.LINE_LIMIT < 4096
+    parsed = json.loads(text)
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "dtype",
+                "data", "config", "roofline", "cpu_baseline", "cpu_baseline_parallel", "permute",
+                "configs_summary", "higher_is_better", "scaling", "vs_baseline"):
+        assert key in parsed, key
+    for key in ("bound", "achieved", "peak", "unit", "frac", "traffic"):
+        assert key in parsed["roofline"], key
+    assert parsed["roofline"]["frac"] == round(140.0 / 157.3, 4)
+    assert parsed["value"] == 140.0 and parsed["ms_per_step"] == 0.9661
+    summ = parsed["configs_summary"]
+    for name in ("c1", "c2a", "c2b", "c2b_1g", "c3", "c4", "c5", "o_rank4", "bgemm16"):
+        assert len(summ[name]) == 3, name
+    assert summ["c2b_1g"] == [6100.0, "GB/s", round(6100.0 / 8000.0, 4)]
+    assert summ["bgemm16"][2] <= 1.0  # priced against the published fp32 vector peak
+    # The detail record keeps what the line leaves out.
+    detail = bench.detail_record(res, Args, train, bgemm16)
+    assert detail["configs"]["c5"]["parts"][0]["plan"]["workgroups"] == 512
+
+
+def test_headline_line_sheds_optional_parts_before_exceeding_the_limit():
+    sys.path.insert(0, str(REPO))
+    import bench
+
+    class Args:
+        steps, warmup, warmup_ms, no_cpu = 20, 50, 30.0, False
+    res, train, bgemm16 = _stub_results()
+    for i in range(200):  # far more workloads than any run has
+        res[f"x{i}"] = res["c1"]
+    old = bench.SUMMARY_ORDER
+    try:
+        bench.SUMMARY_ORDER = tuple(res)
+        line = bench.headline_line(res, Args, train, bgemm16, "d.json")
+    finally:
+        bench.SUMMARY_ORDER = old
+    assert len(json.dumps(line)) <= bench.LINE_LIMIT
+    assert line["value"] == 140.0 and "roofline" in line and "cpu_baseline" in line

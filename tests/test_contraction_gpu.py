@@ -570,12 +570,6 @@ def _rows_check(name, got_rows, want_rows, k, amax, bmax):
     return float(err[worst])
 
 
-def _one_row_per_tile(g, rows, tile=128):
-    """One random row inside every `tile`-row band: every M-tile row of the grid is checked."""
-    return np.array([t + int(g.integers(0, min(tile, rows - t))) for t in range(0, rows, tile)],
-                    dtype=np.uint64)
-
-
 def test_config1_gemm_512_full_oracle(ctx, pool):
     m = n = k = 512
     g = rng(1)
@@ -660,19 +654,13 @@ def test_config5_linear_layer_step(ctx, pool):
     ref = np.zeros(M * N, np.float32)
     oracle.gemm_fast(M, N, K, 1.0, 0.0, x, 0, (K, 1), w, 0, (N, 1), ref, 0, (N, 1))
     _rows_check("Y", y, ref, K, ax, aw)
-    # dX and dW: one whole row inside every 128-row tile band (all 32 M-tiles, every column).
-    rows = _one_row_per_tile(rng(99), M)
+    # dX = dY.W^T and dW = X^T.dY: every element too (about 20 s of the threaded oracle).
     ref = np.zeros(M * K, np.float32)
-    oracle.gemm_fast(M, K, N, 1.0, 0.0, dy, 0, (N, 1), w, 0, (1, N), ref, 0, (K, 1), rows=rows)
-    for r in rows:
-        r = int(r)
-        _rows_check(f"dX row {r}", dx[r * K:(r + 1) * K], ref[r * K:(r + 1) * K], N, ady, aw)
-    rows = _one_row_per_tile(rng(98), K)
+    oracle.gemm_fast(M, K, N, 1.0, 0.0, dy, 0, (N, 1), w, 0, (1, N), ref, 0, (K, 1))
+    _rows_check("dX", dx, ref, N, ady, aw)
     ref = np.zeros(K * N, np.float32)
-    oracle.gemm_fast(K, N, M, 1.0, 1.0, x, 0, (1, K), dy, 0, (N, 1), ref, 0, (N, 1), rows=rows)
-    for r in rows:
-        r = int(r)
-        _rows_check(f"dW row {r}", dw[r * N:(r + 1) * N], ref[r * N:(r + 1) * N], M, ax, ady)
+    oracle.gemm_fast(K, N, M, 1.0, 1.0, x, 0, (1, K), dy, 0, (N, 1), ref, 0, (N, 1))
+    _rows_check("dW", dw, ref, M, ax, ady)
 
 
 def test_gemm_4096_cubed_full_oracle_and_linearity(ctx, pool):

@@ -113,3 +113,54 @@ def test_noalloc_rejects_an_invalid_call_and_launches_nothing(ctx, pool):
                                         ctypes.c_float(0.0), ctypes.byref(cv.to_c()))
     assert st == N.LG_INVALID_ARGUMENT
     assert count() == before
+
+
+def test_noalloc_split_calls_capture_and_replay_like_eager_calls(ctx, pool):
+    """A split-K and a split-dot noalloc call recorded under stream capture: the static array's
+    address was looked up when the context was made, so capture records kernels only. Three
+    replays on new inputs, each bit for bit equal to the eager noalloc call on the same
+    inputs, with eager work and synchronizations between the replays."""
+    import test_graph_gpu as G
+    hip = G.Hip()
+    lib = N.lib()
+    q = ctx.new_stream()
+    g = rng(7300)
+    shapes = [(256, 256, 65536), (1, 1, 1 << 20)]
+    calls = []
+    for m, n, k in shapes:
+        a, b, c = pool.alloc("f32", m * k), pool.alloc("f32", k * n), pool.alloc("f32", m * n)
+        av = L.TensorView.row_major(a, 0, [m, k])
+        bv = L.TensorView.row_major(b, 0, [k, n])
+        cv = L.TensorView.row_major(c, 0, [m, n])
+        from linalg_hip import contraction as C
+        plan = C.plan_gemm(1.0, av, bv, 0.0, cv)
+        assert plan["splits"] > 1 and plan["scratch_bytes"] > 0, plan
+        calls.append((m, n, k, a, b, c, (ctypes.c_float(1.0), ctypes.byref(av.to_c()),
+                                        ctypes.byref(bv.to_c()), ctypes.c_float(0.0),
+                                        ctypes.byref(cv.to_c()))))
+
+    def step(stream):
+        for *_, args in calls:
+            assert lib.lg_encode_gemm_f32_noalloc(ctx.handle, stream, *args) == 0
+
+    graph, exe = hip.capture(q.handle, lambda: step(q.handle))
+    try:
+        for replay in range(3):
+            for m, n, k, a, b, c, _ in calls:
+                a.write((g.standard_normal(m * k) / np.sqrt(k)).astype(np.float32))
+                b.write((g.standard_normal(k * n) / np.sqrt(k)).astype(np.float32))
+                c.write(np.full(m * n, np.nan, np.float32))
+            assert hip.h.hipGraphLaunch(exe, q.handle) == 0
+            q.wait_until_completed()
+            got = [c.read(np.uint32, count=m * n).copy() for m, n, k, a, b, c, _ in calls]
+            for m, n, k, a, b, c, _ in calls:
+                c.write(np.full(m * n, np.nan, np.float32))
+            step(None)
+            ctx.sync()
+            for (m, n, k, a, b, c, _), x in zip(calls, got):
+                assert np.array_equal(x, c.read(np.uint32, count=m * n)), (replay, m, n, k)
+                assert np.all(np.isfinite(x.view(np.float32))), (replay, m, n, k)
+    finally:
+        hip.h.hipGraphExecDestroy(exe)
+        hip.h.hipGraphDestroy(graph)
+        q.close()
