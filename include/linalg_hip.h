@@ -405,7 +405,11 @@ typedef enum lg_plan_kernel {
     LG_KERNEL_DOT = 4,   /* one dot product (chunk) per workgroup */
     LG_KERNEL_OUTER = 5, /* K <= 8: four outputs per thread on the VALU, summed in k order */
     LG_KERNEL_DIRECT = 6, /* 128x128 or 128x256 tile, operand slices loaded straight into LDS */
-    LG_KERNEL_PIPELINED = 7 /* full 128x128 tiles, direct loads, software-pipelined waves */
+    LG_KERNEL_PIPELINED = 7, /* full 128x128 tiles, direct loads, software-pipelined waves */
+    LG_KERNEL_STREAMK = 8   /* full 128x128 tiles spread unevenly over the compute units: one
+                               workgroup per compute unit takes an equal run of the pipelined
+                               kernel's K steps across tiles; a tile two runs share is summed by
+                               the run finishing second (scratch_bytes of the context's scratch) */
 } lg_plan_kernel;
 
 /* Operand load modes of the tiled kernel. */

@@ -195,6 +195,7 @@ lg_status lg_ctx_create(int32_t device, lg_ctx** out) {
         // capture included).
         void* scratch = nullptr;
         hipError_t err = hipMalloc(&scratch, SCRATCH_BYTES);
+        if (err == hipSuccess) err = hipMemset(scratch, 0, SCRATCH_BYTES);  // stream-K counters
         if (err == hipSuccess) err = hipEventCreateWithFlags(&ctx->split_event, hipEventDisableTiming);
         if (err != hipSuccess) {
             if (scratch != nullptr) (void)hipFree(scratch);

@@ -952,8 +952,27 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             }
         }
     }
+    // Stream-K: full 128x128 tiles, at least one per compute unit, that the grids above would
+    // spread unevenly (the busiest compute unit more than 10/9 of the mean: the rank-4 48^6
+    // product, 2304^3, has 324 tiles for 256 compute units) take gemm_f32_sk, which gives each
+    // compute unit an equal run of pipeline steps over 32-deep slices.
+    if (splits == 1 && a_mode != LOAD_S && b_mode != LOAD_S && mm % GEMM_BM == 0 && nn % GEMM_BN == 0 &&
+        k % (PIPE_STAGES * 32) == 0) {
+        const uint64_t t128 = static_cast<uint64_t>(mm / GEMM_BM) * (nn / GEMM_BN) * batch;
+        const uint64_t rounds = (t128 + SK_RANGES - 1) / SK_RANGES;
+        if (t128 >= SK_RANGES && 10 * t128 < 9 * rounds * SK_RANGES) {
+            t.kernel = KERN_SK;
+            t.tile = t.tile_n = GEMM_BM;
+            t.tiles_m = mm / GEMM_BM;
+            t.tiles_n = nn / GEMM_BN;
+            t.slice_k = 32;
+            t.kgroups = 1;
+            info.tile_m = info.tile_n = GEMM_BM;
+        }
+    }
     info.kgroups = t.kgroups;
-    info.kernel = t.kernel == KERN_TILE     ? LG_KERNEL_TILE
+    info.kernel = t.kernel == KERN_SK       ? LG_KERNEL_STREAMK
+                  : t.kernel == KERN_TILE   ? LG_KERNEL_TILE
                   : t.kernel == KERN_PIPE   ? LG_KERNEL_PIPELINED
                   : t.kernel == KERN_DIRECT ? LG_KERNEL_DIRECT
                   : t.kernel == KERN_SMALL  ? LG_KERNEL_SMALL
@@ -963,6 +982,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     info.splits = splits;
     info.k_chunk = chunk;
     info.workgroups = gemm_workgroups(t);
+    if (t.kernel == KERN_SK) info.scratch_bytes = SK_PARTIAL_BYTES;
     if (splits == 1) {
         info.kind = LG_PLAN_TILED;
         return p;
@@ -1016,6 +1036,7 @@ Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, 
 // Device scratch handed to a split or split-dot plan's launches: the partials.
 struct Scratch {
     float* partial = nullptr;
+    uint32_t* counters = nullptr;  // stream-K tickets, SK_COUNTER_BYTES after the partials
 };
 
 bool capturing(hipStream_t s) {
@@ -1025,7 +1046,15 @@ bool capturing(hipStream_t s) {
 }
 
 bool needs_scratch(const Plan& p) {
-    return !p.half && (p.info.kind == LG_PLAN_SPLIT || (p.info.kind == LG_PLAN_DOT && p.dot.splits > 1));
+    return !p.half && (p.info.kind == LG_PLAN_SPLIT || (p.info.kind == LG_PLAN_DOT && p.dot.splits > 1) ||
+                       (p.info.kind == LG_PLAN_TILED && p.gemm.kernel == KERN_SK));
+}
+
+Scratch scratch_at(void* base) {
+    Scratch sc;
+    sc.partial = static_cast<float*>(base);
+    sc.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(base) + SPLIT_PARTIAL_MAX);
+    return sc;
 }
 
 // Enqueues the plan's launches; split and split-dot plans use `sc`.
@@ -1058,6 +1087,10 @@ void launch_plan(lg_ctx* ctx, hipStream_t s, Plan& p, const Scratch& sc) {
             launch_general(ctx, s, p.general);
             return;
         case LG_PLAN_TILED:
+            if (p.gemm.kernel == KERN_SK) {
+                p.gemm.partial = sc.partial;
+                p.gemm.counters = sc.counters;
+            }
             launch_gemm(ctx, s, p.gemm, static_cast<int>(p.info.a_mode),
                         static_cast<int>(p.info.b_mode));
             return;
@@ -1098,9 +1131,7 @@ void execute(lg_ctx* ctx, hipStream_t s, Plan& p) {
             check_hip(hipStreamWaitEvent(s, ctx->split_event, 0), "hipStreamWaitEvent");
         }
     }
-    Scratch sc;
-    sc.partial = static_cast<float*>(ctx->split_scratch);
-    launch_plan(ctx, s, p, sc);
+    launch_plan(ctx, s, p, scratch_at(ctx->split_scratch));
     if (!cap) {
         ctx->split_stream = s;
         if (s != ctx->stream) {
@@ -1132,9 +1163,7 @@ void enqueue_gemm_fixed_scratch(lg_ctx* ctx, void* stream, float alpha, const lg
     }
     set_device(ctx);
     hipStream_t s = pick_stream(ctx, stream);
-    Scratch sc;
-    if (needs_scratch(plan)) sc.partial = scratch(ctx);
-    launch_plan(ctx, s, plan, sc);
+    launch_plan(ctx, s, plan, needs_scratch(plan) ? scratch_at(scratch(ctx)) : Scratch{});
 }
 
 void enqueue_gemm_views(lg_ctx* ctx, hipStream_t s, float alpha, const View& a, const View& b,

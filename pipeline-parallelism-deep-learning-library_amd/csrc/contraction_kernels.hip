@@ -20,6 +20,7 @@ using gemm_detail::gemm_f32_dl;
 using gemm_detail::gemm_f32_mfma;
 using gemm_detail::gemm_f32_kw;
 using gemm_detail::gemm_f32_pl;
+using gemm_detail::gemm_f32_sk;
 using gemm_detail::gemm_f32_small;
 using gemm_detail::gemm_f32_wave;
 using gemm_detail::SMALL_WAVES;
@@ -334,6 +335,19 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         } else {
             hipLaunchKernelGGL((outer_f32<false, false>), dim3(groups), dim3(OUTER_THREADS), 0, s, a);
         }
+    } else if (a.kernel == KERN_SK) {
+        if constexpr (AM != LOAD_S && BMD != LOAD_S) {
+            const uint64_t tiles = static_cast<uint64_t>(a.tiles_m) * a.tiles_n * a.batch;
+            if (a.tile != GEMM_BM || a.tile_n != GEMM_BN || a.m % GEMM_BM != 0 || a.n % GEMM_BN != 0 ||
+                a.slice_k != 32 || a.k % (PIPE_STAGES * 32) != 0 || a.splits != 1 || tiles < groups ||
+                groups != SK_RANGES || a.partial == nullptr || a.counters == nullptr) {
+                fail_invalid("the stream-K GEMM needs full 128x128 tiles, at least one per range, "
+                             "K in whole steps and its scratch");
+            }
+            hipLaunchKernelGGL((gemm_f32_sk<AM, BMD, 32, PIPE_STAGES>), dim3(groups), dim3(256), 0, s, a);
+        } else {
+            fail_invalid("the stream-K GEMM needs a unit-stride axis in both operands");
+        }
     } else if (a.kernel == KERN_PIPE) {
         if constexpr (AM != LOAD_S && BMD != LOAD_S) {
             const uint32_t last = a.k - (a.splits - 1) * a.k_chunk;
@@ -401,6 +415,7 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
 }  // namespace
 
 uint64_t gemm_workgroups(const GemmArgs& a) {
+    if (a.kernel == KERN_SK) return SK_RANGES;
     if (a.kernel == KERN_OUTER) {
         const uint64_t quads = static_cast<uint64_t>(a.batch) * a.m * ((a.n + 3) / 4);
         return std::max<uint64_t>(1, std::min<uint64_t>((quads + OUTER_THREADS - 1) / OUTER_THREADS,
@@ -432,7 +447,7 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
         {{"gemm_f32_pl<K,K>", "gemm_f32_pl<K,MN>", "gemm_f32_pl<K,S>"},
          {"gemm_f32_pl<MN,K>", "gemm_f32_pl<MN,MN>", "gemm_f32_pl<MN,S>"},
          {"gemm_f32_pl<S,K>", "gemm_f32_pl<S,MN>", "gemm_f32_pl<S,S>"}}};
-    if (args.kernel > KERN_PIPE) fail_invalid("unknown GEMM kernel");
+    if (args.kernel > KERN_SK) fail_invalid("unknown GEMM kernel");
     static const char* const deep[3][3] = {
         {"gemm_f32_pl32<K,K>", "gemm_f32_pl32<K,MN>", "gemm_f32_pl32<K,S>"},
         {"gemm_f32_pl32<MN,K>", "gemm_f32_pl32<MN,MN>", "gemm_f32_pl32<MN,S>"},
@@ -445,7 +460,11 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
         {"gemm_f32_pl_n64<K,K>", "gemm_f32_pl_n64<K,MN>", "gemm_f32_pl_n64<K,S>"},
         {"gemm_f32_pl_n64<MN,K>", "gemm_f32_pl_n64<MN,MN>", "gemm_f32_pl_n64<MN,S>"},
         {"gemm_f32_pl_n64<S,K>", "gemm_f32_pl_n64<S,MN>", "gemm_f32_pl_n64<S,S>"}};
-    const char* name = names[args.kernel][a_mode][b_mode];
+    static const char* const sk[3][3] = {
+        {"gemm_f32_sk<K,K>", "gemm_f32_sk<K,MN>", "gemm_f32_sk<K,S>"},
+        {"gemm_f32_sk<MN,K>", "gemm_f32_sk<MN,MN>", "gemm_f32_sk<MN,S>"},
+        {"gemm_f32_sk<S,K>", "gemm_f32_sk<S,MN>", "gemm_f32_sk<S,S>"}};
+    const char* name = args.kernel == KERN_SK ? sk[a_mode][b_mode] : names[args.kernel][a_mode][b_mode];
     if (args.kernel == KERN_PIPE && args.tile == GEMM_BM && args.tile_n == PIPE_NARROW_N) {
         name = narrow[a_mode][b_mode];
     } else if (args.kernel == KERN_PIPE && args.tile == GEMM_SMALL_TILE) {

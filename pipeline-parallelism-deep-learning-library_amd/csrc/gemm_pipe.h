@@ -58,6 +58,148 @@ constexpr int pl_workgroups() {
     return by_lds < 3 ? by_lds : 3;
 }
 
+// The pipelined loop of one 128 x 64*FN output tile: `ktiles` slices of BK along K from A and B
+// (pointers at the tile's first row or column and its first k), added into acc. Leaves loads of
+// the last slice in flight into the LDS stages: a caller that reuses the stages waits for them.
+template <int AM, int BMD, int BK, int NS, int FN>
+__device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, const float* A,
+                                             const float* B, uint32_t ktiles,
+                                             floatx16 (&acc)[2][FN]) {
+    static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
+    static_assert(FN == 1 || FN == 2, "128x64 or 128x128 tiles");
+    constexpr int T = 256, NW = 4, FM = 2, RA = 128, RB = 64 * FN;
+    (void)T;
+    using GA = DlGeo<RA, BK, T>;
+    using GB = DlGeo<RB, BK, T>;
+    constexpr int PER = GA::LOADS + GB::LOADS;  // load instructions per slice per thread
+    constexpr int G = BK / 8;                   // fragment groups per slice
+    constexpr int MG = 4 * FM * FN;             // MFMAs per group
+    static_assert(G >= 2 && G % 2 == 0, "groups alternate between two fragment register sets");
+    static_assert(NS >= 2 && (NS - 1) * PER < 64, "stages (vmcnt counts at most 63)");
+    // Reads of one group after the first RM MFMAs of the previous group, RPM after each; the
+    // first group's loads, up to two after each of NV MFMAs, from the tenth MFMA on where the
+    // group is that long (earlier positions measured 2-4 % slower on batched 1024^3 products).
+    constexpr int RD = pl_reads<AM, BMD, FM, FN>();
+    constexpr int RPM = RD > MG * 3 / 4 ? 2 : 1;
+    constexpr int RM = (RD + RPM - 1) / RPM;
+    constexpr int NV = (PER + 1) / 2;
+    constexpr int VF0 = 10 - RM < MG - RM - NV ? 10 - RM : MG - RM - NV;
+    constexpr int VF = VF0 > 0 ? VF0 : 0;
+    static_assert(RM + VF + NV <= MG, "MFMAs of a group");
+
+    float* As = smem;
+    float* Bs = smem + NS * GA::ST;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / 2, wn = wave % 2;
+    const int lr = lane & 31, h = lane >> 5;
+
+    const float alpha_a = p.scale_b ? 1.0f : p.alpha;
+    const float alpha_b = p.scale_b ? p.alpha : 1.0f;
+
+    int64_t sa[GA::LOADS], sb[GB::LOADS];
+#pragma unroll
+    for (int i = 0; i < GA::LOADS; ++i) sa[i] = dl_src<AM, RA, BK>((i * NW + wave) * 64 + lane, p.a_sm, p.a_sk);
+#pragma unroll
+    for (int i = 0; i < GB::LOADS; ++i) sb[i] = dl_src<BMD, RB, BK>((i * NW + wave) * 64 + lane, p.b_sn, p.b_sk);
+    const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
+    const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
+    // Slice kt into `stage`.
+    auto issue = [&](uint32_t kt, int stage) {
+        float* as = As + stage * GA::ST;
+        float* bs = Bs + stage * GB::ST;
+#pragma unroll
+        for (int i = 0; i < GA::LOADS; ++i) dl_copy16(A + sa[i] + kt * a_step, as + (i * NW + wave) * 256);
+#pragma unroll
+        for (int i = 0; i < GB::LOADS; ++i) dl_copy16(B + sb[i] + kt * b_step, bs + (i * NW + wave) * 256);
+    };
+
+    auto run = [&](auto scale) {
+        constexpr bool SCALE = decltype(scale)::value;
+        floatx4 fa[2][FM], fb[2][FN];
+        // Fragment group g of the slice in `stage` into register set `set`.
+        auto read = [&](int set, int g, int stage) {
+            dl_frag<AM, RA, BK, FM>(fa[set], As + stage * GA::ST, wm * 32 * FM, g, lr, h);
+            dl_frag<BMD, RB, BK, FN>(fb[set], Bs + stage * GB::ST, wn * 32 * FN, g, lr, h);
+            if constexpr (SCALE) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[set][i] = fa[set][i] * alpha_a;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[set][j] = fb[set][j] * alpha_b;
+            }
+        };
+        // Slices 0 .. NS-2 in flight; slice step kt then issues slice kt + NS - 1 into the
+        // stage slice kt - 1 used (clamped to the last slice), so at the barrier of step kt the
+        // loads issued after slice kt + 1's are always those of the NS - 2 slices behind it.
+#pragma unroll
+        for (int s = 0; s + 1 < NS; ++s) issue(min(static_cast<uint32_t>(s), ktiles - 1), s);
+        wait_vm<(NS - 2) * PER>();
+        __builtin_amdgcn_s_barrier();
+        read(0, 0, 0);
+        for (uint32_t k0 = 0; k0 < ktiles; k0 += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+                const uint32_t kt = k0 + u;
+#pragma unroll
+                for (int g = 0; g + 1 < G; ++g) {
+                    read((g + 1) & 1, g + 1, u);
+                    if (g == 0) issue(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                    mfma_group<FM, FN>(acc, fa[g & 1], fb[g & 1]);
+                    pl_after_each_mfma<RM, 0x100, RPM>();
+                    if (g == 0) {
+                        if constexpr (VF > 0) __builtin_amdgcn_sched_group_barrier(0x008, VF, 0);
+                        pl_after_each_mfma<NV, 0x010, 2>();
+                        __builtin_amdgcn_sched_group_barrier(0x008, MG - RM - VF - NV, 0);
+                    } else {
+                        __builtin_amdgcn_sched_group_barrier(0x008, MG - RM, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // Slice kt + 1 landed for every wave, slice kt read by every wave.
+                wait_vm<(NS - 2) * PER>();
+                wait_lgkm0();
+                __builtin_amdgcn_s_barrier();
+                constexpr int L = (G - 1) & 1;
+                read(0, 0, (u + 1) % NS);  // past the last slice: unused
+                mfma_group<FM, FN>(acc, fa[L], fb[L]);
+                pl_after_each_mfma<RM, 0x100, RPM>();
+                __builtin_amdgcn_sched_group_barrier(0x008, MG - RM, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    if (alpha_a != 1.0f || alpha_b != 1.0f) {
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
+    }
+
+}
+
+// Stores one 128 x 64*FN tile of C (plane bi, first row m0, first column n0): beta * C + acc,
+// or acc alone when beta is 0 (C never read).
+template <int FN>
+__device__ __forceinline__ void pl_store_c(const GemmArgs& p, const floatx16 (&acc)[2][FN],
+                                           uint32_t bi, uint32_t m0, uint32_t n0) {
+    constexpr int FM = 2;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / 2, wn = wave % 2;
+    const int lr = lane & 31, h = lane >> 5;
+    float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t row = m0 + wm * 32 * FM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                const uint32_t col = n0 + wn * 32 * FN + j * 32 + lr;
+                float* q = C + static_cast<int64_t>(row) * p.c_sm + static_cast<int64_t>(col) * p.c_sn;
+                float v = acc[i][j][r];
+                if (p.beta != 0.0f) v = p.beta * *q + v;
+                *q = v;
+            }
+}
+
 template <int AM, int BMD, int BK, int NS, int FN = 2>
 __global__ __launch_bounds__(256, (pl_workgroups<BK, NS, FN>()))
 void gemm_f32_pl(GemmArgs p) {
@@ -216,6 +358,140 @@ void gemm_f32_pl(GemmArgs p) {
                 if (p.beta != 0.0f) v = p.beta * *q + v;
                 *q = v;
             }
+}
+
+// gemm_f32_sk<AM, BMD, BK, NS>: stream-K over the pipelined loop of full 128x128 tiles. The T
+// output tiles of S = K / (NS * BK) pipeline steps each make T * S steps, cut into gridDim.x
+// = G contiguous runs as even as integers allow (run r: [r * T * S / G, (r + 1) * T * S / G)),
+// so every compute unit gets the same work whatever T is. The planner keeps every run at
+// least S long (T >= G), so a tile's steps fall to at most two runs: a tile split at run
+// boundary b (1 <= b < G) is the last part of run b - 1 and the first part of run b. The
+// first part, which run b takes at its start, covers the tile's first K steps and the last
+// part, which run b - 1 takes at its end, the rest: every run starts at k = 0 like a plain
+// grid, and the last part usually finds the first one done. The two sums meet in slots 2b
+// (last part) and 2b + 1 (first part) of `partial` and a ticket counter, counters[b]:
+//   * the first part stores its sum, then takes a ticket;
+//   * the last part first reads the counter: when the first part's ticket is there, it adds
+//     that part's sum to its own at once; otherwise it stores its sum and takes a ticket too;
+//   * whichever holds the second ticket adds the other's sum to its own (a + b and b + a are
+//     the same float), applies beta * C, stores the tile and clears the counter for the next
+//     launch.
+// No workgroup waits for another, and every result depends on the shape alone. Tiles a run
+// covers whole are stored directly. The sums and tickets move through device-scope (agent)
+// accesses, which no XCD's L2 keeps a stale copy of: relaxed atomic stores acknowledged before
+// the ticket is taken, relaxed atomic loads issued only after the ticket is seen. No fence
+// writes back or invalidates an XCD's L2, which holds the operand panels of the other runs.
+// Runs are numbered in XCD order (run r on XCD r * 8 / G), so consecutive runs, which share
+// tiles and operand panels, sit on one XCD. One workgroup per compute unit (BK = 32); partial
+// holds 2G slots of 128x128 floats.
+template <int AM, int BMD, int BK, int NS>
+__global__ __launch_bounds__(256, 1) void gemm_f32_sk(GemmArgs p) {
+    constexpr int FN = 2, RA = 128, RB = 128, SLOT = 128 * 128;  // floats per partial slot
+    using GA = DlGeo<RA, BK, 256>;
+    using GB = DlGeo<RB, BK, 256>;
+    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
+    __shared__ uint32_t ticket;
+    const int tid = threadIdx.x;
+
+    const uint32_t G = gridDim.x, bid = blockIdx.x;
+    const uint32_t xcd = bid & 7u, slot_in = bid >> 3, q8 = G >> 3, r8 = G & 7u;
+    const uint32_t r = xcd < r8 ? xcd * (q8 + 1) + slot_in : r8 * (q8 + 1) + (xcd - r8) * q8 + slot_in;
+    const uint32_t per_plane = p.tiles_m * p.tiles_n;
+    const uint64_t T = static_cast<uint64_t>(per_plane) * p.batch;
+    const uint32_t S = p.k / (NS * BK);
+    const uint64_t steps = T * S;
+    uint64_t x = static_cast<uint64_t>(r) * steps / G;
+    const uint64_t end = static_cast<uint64_t>(r + 1) * steps / G;
+
+    auto add_other = [&](floatx16 (&acc)[2][FN], const float* other) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    acc[i][j][e] = acc[i][j][e] + __hip_atomic_load(other + ((i * FN + j) * 16 + e) * 256,
+                                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+    };
+
+    while (x < end) {
+        const uint64_t t = x / S;
+        const uint32_t s0 = static_cast<uint32_t>(x - t * S);
+        const uint32_t s1 = static_cast<uint32_t>(min(static_cast<uint64_t>(S), s0 + (end - x)));
+        const uint32_t len = s1 - s0;
+        const bool whole = len == S;
+        const bool first_part = s0 > 0;            // the run started inside this tile
+        const uint32_t b = first_part ? r : r + 1;  // the run boundary splitting the tile
+        // K steps of this part: the first part from k = 0, the last part the rest.
+        const uint32_t k0 = whole || first_part ? 0 : S - len;
+        // Tile t: plane, then groups of eight tile rows walked column by column (decode_tile's
+        // order), so a run of consecutive tiles reuses A and B panels in the XCD's L2.
+        const uint32_t bi = static_cast<uint32_t>(t / per_plane);
+        const uint32_t tp = static_cast<uint32_t>(t - static_cast<uint64_t>(bi) * per_plane);
+        const uint32_t group = tp / (8 * p.tiles_n), first_m = group * 8;
+        const uint32_t gm = min(p.tiles_m - first_m, 8u), in_group = tp - group * 8 * p.tiles_n;
+        const uint32_t m0 = (first_m + in_group % gm) * RA, n0 = (in_group / gm) * RB;
+        const uint32_t kb = k0 * NS * BK;
+        const float* A = p.a + static_cast<int64_t>(bi) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm +
+                         static_cast<int64_t>(kb) * p.a_sk;
+        const float* B = p.b + static_cast<int64_t>(bi) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn +
+                         static_cast<int64_t>(kb) * p.b_sk;
+        floatx16 acc[2][FN];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        pl_tile_loop<AM, BMD, BK, NS, FN>(p, smem, A, B, len * NS, acc);
+
+        if (whole) {
+            pl_store_c<FN>(p, acc, bi, m0, n0);
+        } else {
+            float* mine = p.partial + static_cast<int64_t>(2 * b + (first_part ? 1 : 0)) * SLOT + tid;
+            const float* other = p.partial + static_cast<int64_t>(2 * b + (first_part ? 0 : 1)) * SLOT + tid;
+            bool done = false;
+            if (!first_part) {
+                if (tid == 0) {
+                    ticket = __hip_atomic_load(p.counters + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __syncthreads();
+                done = ticket == 1;  // the first part's sum is complete
+                __syncthreads();     // every thread has read `ticket` before it is reused
+            }
+            if (!done) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            __hip_atomic_store(mine + ((i * FN + j) * 16 + e) * 256, acc[i][j][e],
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                wait_vm<0>();  // every store of this thread acknowledged
+                __syncthreads();
+                if (tid == 0) {
+                    ticket = __hip_atomic_fetch_add(p.counters + b, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __syncthreads();
+                done = ticket == 1;
+            }
+            if (done) {
+                add_other(acc, other);
+                pl_store_c<FN>(p, acc, bi, m0, n0);
+                if (tid == 0) __hip_atomic_store(p.counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        x += len;
+        // The loop leaves loads of its last slice in flight into the stages: let them land,
+        // and every wave finish reading, before the next tile's loads reuse the stages.
+        wait_vm<0>();
+        wait_lgkm0();
+        __syncthreads();
+    }
 }
 
 // gemm_f32_kw<AM, BMD, BK, NS>: a 64x64 output tile per workgroup whose four waves each

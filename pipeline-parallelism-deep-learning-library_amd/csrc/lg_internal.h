@@ -141,7 +141,8 @@ enum GemmKernel : uint32_t {
     KERN_WAVE = 2,   // gemm_f32_wave: one 32x32 tile per wave, four tiles per workgroup
     KERN_OUTER = 3,  // outer_f32: K <= OUTER_MAX_K on the VALU, four outputs per thread
     KERN_DIRECT = 4, // gemm_f32_dl: 128x128 or 128x256 tiles, slices loaded straight into LDS
-    KERN_PIPE = 5    // gemm_f32_pl (full 128x128 tiles) / gemm_f32_kw (full 64x64 tiles): software-pipelined direct loads
+    KERN_PIPE = 5,   // gemm_f32_pl (full 128x128 tiles) / gemm_f32_kw (full 64x64 tiles): software-pipelined direct loads
+    KERN_SK = 6      // gemm_f32_sk: stream-K over full 128x128 tiles, one workgroup per compute unit
 };
 // N extent of the wide direct-load tile (eight waves, 128x256).
 constexpr uint32_t GEMM_WIDE_N = 256;
@@ -158,7 +159,7 @@ struct GemmArgs {
     const float* a;  // element pointer of A's view offset
     const float* b;
     float* c;
-    float* partial;  // split-K partials [batch][splits][m][n], or null
+    float* partial;  // split-K partials [batch][splits][m][n], or null; KERN_SK: 2G tile slots
     int64_t a_sb, a_sm, a_sk;
     int64_t b_sb, b_sn, b_sk;
     int64_t c_sb, c_sm, c_sn;
@@ -181,6 +182,7 @@ struct GemmArgs {
     uint32_t kgroups;
     // KERN_PIPE: K depth of one LDS slice, 16 or 32.
     uint32_t slice_k;
+    uint32_t* counters;  // KERN_SK: one ticket counter per range boundary, zero between launches
 };
 
 // Dot products (M = N = 1): C[b] = beta*C[b] + sum_k (alpha*a[b][k])*b[b][k]. Split along K
@@ -203,7 +205,16 @@ constexpr uint32_t DOT_TARGET = 2048;      // workgroups the split dot path aims
 // The per-context scratch of split partials. Plans never need more than SPLIT_PARTIAL_MAX
 // bytes of partials (the planner caps the split count to fit).
 constexpr uint64_t SPLIT_PARTIAL_MAX = 32ull << 20;
-constexpr uint64_t SCRATCH_BYTES = SPLIT_PARTIAL_MAX;
+// Stream-K (KERN_SK): SK_RANGES workgroups, one per compute unit of the part (a constant, so
+// plans and results depend on the shape alone); 2 * SK_RANGES partial slots of a 128x128 tile
+// fill SPLIT_PARTIAL_MAX exactly. Its ticket counters follow the partials in the scratch,
+// zeroed when the scratch is made and cleared again by every launch that uses them.
+constexpr uint32_t SK_RANGES = 256;
+constexpr uint64_t SK_PARTIAL_BYTES = 2ull * SK_RANGES * 128 * 128 * sizeof(float);
+static_assert(SK_PARTIAL_BYTES <= SPLIT_PARTIAL_MAX, "stream-K slots fit the partials");
+constexpr uint64_t SK_COUNTER_BYTES = 4096;
+static_assert(SK_COUNTER_BYTES >= SK_RANGES * sizeof(uint32_t), "one counter per boundary");
+constexpr uint64_t SCRATCH_BYTES = SPLIT_PARTIAL_MAX + SK_COUNTER_BYTES;
 
 struct ReduceArgs {
     const float* partial;

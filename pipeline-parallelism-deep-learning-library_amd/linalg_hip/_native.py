@@ -22,7 +22,7 @@ CORE_ERRORS = ["Ok", "Shape", "Dtype", "UnsupportedLayout", "UnsupportedDevice",
 LG_DTYPE_F32, LG_DTYPE_F16, LG_DTYPE_BF16 = 1, 2, 3
 LG_WIRE_HEADER_MAX = 48
 PLAN_KINDS = ["empty", "zero", "scale", "tiled", "split", "general", "dot"]
-PLAN_KERNELS = ["none", "tile", "small", "wave", "dot", "outer", "direct", "pipelined"]
+PLAN_KERNELS = ["none", "tile", "small", "wave", "dot", "outer", "direct", "pipelined", "streamk"]
 LOAD_MODES = ["k", "mn", "strided"]
 PERMUTE_KINDS = ["empty", "copy", "tile"]
 

@@ -290,9 +290,10 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_contract(1.0, (dense([48] * 4), "ijkl"), (dense([48] * 4), "klmn"), 0.0,
                         (dense([48] * 4), "ijmn"))
     assert (p["kind"], p["groups"], p["m"], p["n"], p["k"]) == ("tiled", 1, 2304, 2304, 2304)
-    # 324 tiles of 128x128 spread unevenly over 256 compute units: 648 128x64 tiles fill three
-    # pipelined workgroups per compute unit in one round.
-    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (128, 64), 648)
+    # 324 tiles of 128x128 spread unevenly over 256 compute units: stream-K, 256 equal runs of
+    # pipeline steps, 2 x 256 tile slots of scratch.
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("streamk", (128, 128), 256)
+    assert p["scratch_bytes"] == 2 * 256 * 128 * 128 * 4
     # Not full 128x64 tiles, or K not in whole 64-deep steps: 64x64 tiles (1296).
     for m, n, k in [(2300, 2304, 2304), (2304, 2304, 2000)]:
         p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
@@ -592,3 +593,23 @@ def test_plans_without_a_k_split_report_one_wave_group():
         assert p["kgroups"] == 1, p
         if kernel:
             assert p["kernel"] == kernel, p
+
+
+def test_stream_k_plans():
+    """Stream-K takes full 128x128 tiles, at least 256 of them, K in whole 128-deep steps, when a
+    plain grid would leave the busiest compute unit more than 10/9 of the mean; balanced grids
+    keep the pipelined kernel."""
+    def plan(m, n, k, batch=1):
+        bs = [batch] if batch > 1 else []
+        return C.plan_gemm(1.0, dense(bs + [m, k]), dense(bs + [k, n]), 0.0, dense(bs + [m, n]))
+    for m, n, k, batch in [(2304, 2304, 2304, 1), (2560, 2560, 1024, 1), (3072, 3072, 640, 1),
+                           (1280, 1280, 512, 3), (4096, 2560, 4096, 1)]:
+        p = plan(m, n, k, batch)
+        assert (p["kind"], p["kernel"], p["tile"], p["workgroups"], p["splits"]) == \
+            ("tiled", "streamk", (128, 128), 256, 1), (m, n, k, batch, p)
+    # Balanced grids (whole rounds of 256 tiles, or within 10/9 of them) stay pipelined.
+    for m, n, k in [(4096, 4096, 4096), (2048, 2048, 2048), (4096, 3840, 1024)]:
+        assert plan(m, n, k)["kernel"] == "pipelined", (m, n, k)
+    # K not in whole 128-deep steps, ragged tiles, or fewer tiles than compute units: no stream-K.
+    for m, n, k in [(2304, 2304, 2000), (2300, 2304, 2304), (1536, 1536, 1536)]:
+        assert plan(m, n, k)["kernel"] != "streamk", (m, n, k)

@@ -914,14 +914,15 @@ def test_pipelined_kernel_split_along_k(ctx, pool, m, n, k, ta, tb, tc, splits):
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
-@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2304, 2304, 256, False, False, False),
-                                            (2048, 3072, 128, True, False, False),
-                                            (3072, 2048, 192, False, True, True),
-                                            (2304, 2304, 64, True, True, False)])
+@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(2304, 2240, 256, False, False, False),
+                                            (2048, 2880, 128, True, False, False),
+                                            (2880, 2048, 192, False, True, True),
+                                            (2304, 2240, 64, True, True, False)])
 def test_pipelined_128x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
-    """Grids of 648-768 full 128x64 tiles (three pipelined workgroups per compute unit in one
-    round): (K, MN), (MN, MN), the swapped (K, K) product with C column-major, (MN, K) with K of
-    one pipeline step; alpha != 1 with beta != 0; against crates/cpu on every element, the same
+    """Grids of 512-768 full 128x64 tiles whose N is not a multiple of 128 (full 128x128 grids
+    of that size take stream-K): three pipelined workgroups per compute unit in one round.
+    (K, MN), (MN, MN), the swapped (K, K) product with C column-major, (MN, K) with K of one
+    pipeline step; alpha != 1 with beta != 0; against crates/cpu on every element, the same
     bits over two runs."""
     pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
     la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
