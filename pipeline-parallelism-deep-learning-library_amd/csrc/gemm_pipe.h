@@ -389,8 +389,11 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_sk(GemmArgs p) {
     constexpr int FN = 2, RA = 128, RB = 128, SLOT = 128 * 128;  // floats per partial slot
     using GA = DlGeo<RA, BK, 256>;
     using GB = DlGeo<RB, BK, 256>;
-    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
-    __shared__ uint32_t ticket;
+    // The ticket word lives in the stages' own LDS array, past the stages: a second LDS object
+    // would keep the compiler from telling the stages' direct loads apart from its fragment
+    // reads, and it would then wait for every load in flight before each read.
+    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST) + 4];
+    uint32_t& ticket = *reinterpret_cast<uint32_t*>(smem + NS * (GA::ST + GB::ST));
     const int tid = threadIdx.x;
 
     const uint32_t G = gridDim.x, bid = blockIdx.x;
