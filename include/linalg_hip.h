@@ -196,7 +196,8 @@ lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const l
 /* No counterpart in the reference: lg_encode_gemm_f32 for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
  * Same arguments, validation, plans and results as lg_encode_gemm_f32. It allocates nothing:
- * split-K and split-dot partials live in a static device array of 32 MiB that each GPU holds
+ * split-K, split-dot and stream-K partials live in a static device array of 32 MiB (plus
+ * 4 KiB of stream-K ticket counters) that each GPU holds from the first lg_ctx_create on it
  * until the process ends (no plan needs more; a product that did would fail with
  * LG_INVALID_ARGUMENT before launching anything). Every call on one GPU shares that GPU's
  * array, so calls that overlap on one GPU race on it and must be ordered by the caller (one

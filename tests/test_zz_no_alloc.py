@@ -1,6 +1,7 @@
 """lg_encode_gemm_f32_noalloc against lg_encode_gemm_f32, through the C ABI.
 
-The entry point allocates nothing: split-K and split-dot partials live in a static device
+The entry point allocates nothing: split-K, split-dot and stream-K partials (and stream-K's
+ticket counters) live in a static device
 array. Its results must be the existing entry point's (the same plans, so bit for bit) and
 pass the north-star bound against the crates/cpu restatement, over calls in a row whose later
 inputs are smaller (the array keeps the last call's contents, so stale partials would
@@ -29,6 +30,7 @@ SHAPES = [
     (1, 1, 100003),     # a smaller split dot
     (300, 200, 100),    # one tiled launch, no scratch
     (256, 128, 9000),   # split-K again on 64x64 tiles, fewer and smaller partials
+    (2304, 2304, 1152), # stream-K: 324 tiles over 256 runs, tile sums and tickets in the array
 ]
 
 
@@ -116,8 +118,9 @@ def test_noalloc_rejects_an_invalid_call_and_launches_nothing(ctx, pool):
 
 
 def test_noalloc_split_calls_capture_and_replay_like_eager_calls(ctx, pool):
-    """A split-K and a split-dot noalloc call recorded under stream capture: the static array's
-    address was looked up when the context was made, so capture records kernels only. Three
+    """A split-K, a split-dot and a stream-K noalloc call recorded under stream capture: the
+    static array's address was looked up when the context was made, so capture records kernels
+    only (the stream-K tickets are left at zero by every launch). Three
     replays on new inputs, each bit for bit equal to the eager noalloc call on the same
     inputs, with eager work and synchronizations between the replays."""
     import test_graph_gpu as G
@@ -125,7 +128,7 @@ def test_noalloc_split_calls_capture_and_replay_like_eager_calls(ctx, pool):
     lib = N.lib()
     q = ctx.new_stream()
     g = rng(7300)
-    shapes = [(256, 256, 65536), (1, 1, 1 << 20)]
+    shapes = [(256, 256, 65536), (1, 1, 1 << 20), (2304, 2304, 1152)]
     calls = []
     for m, n, k in shapes:
         a, b, c = pool.alloc("f32", m * k), pool.alloc("f32", k * n), pool.alloc("f32", m * n)
@@ -134,7 +137,7 @@ def test_noalloc_split_calls_capture_and_replay_like_eager_calls(ctx, pool):
         cv = L.TensorView.row_major(c, 0, [m, n])
         from linalg_hip import contraction as C
         plan = C.plan_gemm(1.0, av, bv, 0.0, cv)
-        assert plan["splits"] > 1 and plan["scratch_bytes"] > 0, plan
+        assert plan["scratch_bytes"] > 0, plan  # split-K, split dot, stream-K
         calls.append((m, n, k, a, b, c, (ctypes.c_float(1.0), ctypes.byref(av.to_c()),
                                         ctypes.byref(bv.to_c()), ctypes.c_float(0.0),
                                         ctypes.byref(cv.to_c()))))
