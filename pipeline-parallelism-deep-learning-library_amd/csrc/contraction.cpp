@@ -952,6 +952,17 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
             }
         }
     }
+    // Full 128x128 pipelined tiles on 16-deep slices (grids of at least two workgroups per
+    // compute unit) with A contiguous along K pair up along M into 256x128 tiles of eight waves
+    // (gemm_f32_pl256, one workgroup per compute unit): the same waves, 3/4 of the operand
+    // loads (4096^3: 142 -> 144-145 TFLOP/s, config 3 134 -> 136-138, config 5's Y 143 -> 145).
+    // A contiguous along M keeps 128x128 tiles (config 5's dW: 138 against 135).
+    if (t.kernel == KERN_PIPE && t.tile == GEMM_BM && t.tile_n == GEMM_BN && t.slice_k == 16 &&
+        splits == 1 && a_mode == LOAD_K && mm % PIPE_TALL_M == 0 && k % (PIPE_STAGES * 16) == 0) {
+        t.tile = PIPE_TALL_M;
+        t.tiles_m = mm / PIPE_TALL_M;
+        info.tile_m = PIPE_TALL_M;
+    }
     // Stream-K: full 128x128 tiles, at least one per compute unit, that the grids above would
     // spread unevenly (the busiest compute unit more than 10/9 of the mean: the rank-4 48^6
     // product, 2304^3, has 324 tiles for 256 compute units) take gemm_f32_sk, which gives each

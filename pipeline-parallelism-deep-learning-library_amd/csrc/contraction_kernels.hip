@@ -20,6 +20,7 @@ using gemm_detail::gemm_f32_dl;
 using gemm_detail::gemm_f32_mfma;
 using gemm_detail::gemm_f32_kw;
 using gemm_detail::gemm_f32_pl;
+using gemm_detail::gemm_f32_pl256;
 using gemm_detail::gemm_f32_sk;
 using gemm_detail::gemm_f32_small;
 using gemm_detail::gemm_f32_wave;
@@ -361,6 +362,14 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
                 return;
             }
             const uint32_t step = PIPE_STAGES * a.slice_k;
+            if (a.tile == PIPE_TALL_M) {
+                if (a.tile_n != GEMM_BN || a.m % PIPE_TALL_M != 0 || a.n % GEMM_BN != 0 || a.slice_k != 16 ||
+                    a.splits != 1 || a.k % step != 0) {
+                    fail_invalid("the 256x128 pipelined GEMM needs full tiles and K in whole steps");
+                }
+                hipLaunchKernelGGL((gemm_f32_pl256<AM, BMD, 16, PIPE_STAGES>), dim3(groups), dim3(512), 0, s, a);
+                return;
+            }
             if (a.tile_n == PIPE_NARROW_N) {
                 if (a.tile != GEMM_BM || a.m % GEMM_BM != 0 || a.n % PIPE_NARROW_N != 0 || a.slice_k != 16 ||
                     a.k_chunk % step != 0 || last % step != 0) {
@@ -465,7 +474,13 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
         {"gemm_f32_sk<MN,K>", "gemm_f32_sk<MN,MN>", "gemm_f32_sk<MN,S>"},
         {"gemm_f32_sk<S,K>", "gemm_f32_sk<S,MN>", "gemm_f32_sk<S,S>"}};
     const char* name = args.kernel == KERN_SK ? sk[a_mode][b_mode] : names[args.kernel][a_mode][b_mode];
-    if (args.kernel == KERN_PIPE && args.tile == GEMM_BM && args.tile_n == PIPE_NARROW_N) {
+    static const char* const tall[3][3] = {
+        {"gemm_f32_pl256<K,K>", "gemm_f32_pl256<K,MN>", "gemm_f32_pl256<K,S>"},
+        {"gemm_f32_pl256<MN,K>", "gemm_f32_pl256<MN,MN>", "gemm_f32_pl256<MN,S>"},
+        {"gemm_f32_pl256<S,K>", "gemm_f32_pl256<S,MN>", "gemm_f32_pl256<S,S>"}};
+    if (args.kernel == KERN_PIPE && args.tile == PIPE_TALL_M) {
+        name = tall[a_mode][b_mode];
+    } else if (args.kernel == KERN_PIPE && args.tile == GEMM_BM && args.tile_n == PIPE_NARROW_N) {
         name = narrow[a_mode][b_mode];
     } else if (args.kernel == KERN_PIPE && args.tile == GEMM_SMALL_TILE) {
         name = kw[a_mode][b_mode];

@@ -58,17 +58,18 @@ constexpr int pl_workgroups() {
     return by_lds < 3 ? by_lds : 3;
 }
 
-// The pipelined loop of one 128 x 64*FN output tile: `ktiles` slices of BK along K from A and B
-// (pointers at the tile's first row or column and its first k), added into acc. Leaves loads of
-// the last slice in flight into the LDS stages: a caller that reuses the stages waits for them.
-template <int AM, int BMD, int BK, int NS, int FN>
+// The pipelined loop of one (64*WM) x (64*FN) output tile, WM x 2 waves of 2 x FN blocks (the
+// loop of gemm_f32_pl): `ktiles` slices of BK along K from A and B (pointers at the tile's first
+// row or column and its first k), added into acc. Leaves loads of the last slice in flight into
+// the LDS stages: a caller that reuses the stages waits for them.
+template <int AM, int BMD, int BK, int NS, int FN, int WM = 2>
 __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, const float* A,
                                              const float* B, uint32_t ktiles,
                                              floatx16 (&acc)[2][FN]) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
-    static_assert(FN == 1 || FN == 2, "128x64 or 128x128 tiles");
-    constexpr int T = 256, NW = 4, FM = 2, RA = 128, RB = 64 * FN;
-    (void)T;
+    static_assert(FN == 1 || FN == 2, "64*WM x 64 or 64*WM x 128 tiles");
+    static_assert(WM == 2 || WM == 4, "WM x 2 waves of 2 x FN blocks");
+    constexpr int FM = 2, NW = 2 * WM, T = 64 * NW, RA = 32 * FM * WM, RB = 64 * FN;
     using GA = DlGeo<RA, BK, T>;
     using GB = DlGeo<RB, BK, T>;
     constexpr int PER = GA::LOADS + GB::LOADS;  // load instructions per slice per thread
@@ -358,6 +359,34 @@ void gemm_f32_pl(GemmArgs p) {
                 if (p.beta != 0.0f) v = p.beta * *q + v;
                 *q = v;
             }
+}
+
+// gemm_f32_pl256<AM, BMD, BK, NS>: the pipelined loop on full 256x128 tiles with eight waves
+// (4x2, each 2x2 blocks of 32x32 as in gemm_f32_pl). The waves keep gemm_f32_pl's fragment
+// reads per MFMA and two waves per SIMD, while one workgroup's stages serve twice the rows of
+// B: it loads 3/4 of the operand bytes per FLOP that two 128x128 workgroups do. One workgroup
+// per compute unit (96 KiB of stages). Every K in whole steps of NS slices; M a multiple of 256,
+// N of 128; no split.
+template <int AM, int BMD, int BK, int NS>
+__global__ __launch_bounds__(512, 1) void gemm_f32_pl256(GemmArgs p) {
+    constexpr int FN = 2, RA = 256, RB = 128;
+    using GA = DlGeo<RA, BK, 512>;
+    using GB = DlGeo<RB, BK, 512>;
+    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
+    uint32_t plane, tm, tn;
+    decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    const uint32_t m0 = tm * RA, n0 = tn * RB;
+    const float* A = p.a + static_cast<int64_t>(plane) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm;
+    const float* B = p.b + static_cast<int64_t>(plane) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn;
+    floatx16 acc[2][FN];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    pl_tile_loop<AM, BMD, BK, NS, FN, 4>(p, smem, A, B, p.k / BK, acc);
+    pl_store_c<FN>(p, acc, plane, m0, n0);
 }
 
 // gemm_f32_sk<AM, BMD, BK, NS>: stream-K over the pipelined loop of full 128x128 tiles. The T

@@ -944,20 +944,22 @@ def test_pipelined_128x64_tiles(ctx, pool, m, n, k, ta, tb, tc):
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
 
 
-@pytest.mark.parametrize("m,n,k,ta,tb,tc", [(4096, 2048, 192, False, False, False),
-                                            (4096, 2048, 128, True, False, False),
-                                            (2048, 4096, 256, False, True, True),
-                                            (4096, 2048, 64, True, True, False),
-                                            (4096, 2048, 4224, False, True, False),
-                                            (2048, 2048, 2048, False, False, False),
-                                            (2048, 2048, 1152, True, True, True)])
-def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc):
-    """Full 128x128 tiles on the software-pipelined kernel. Grids of 512 tiles (16-deep
+@pytest.mark.parametrize("m,n,k,ta,tb,tc,tile_m", [(4096, 2048, 192, False, False, False, 256),
+                                                   (4096, 2048, 128, True, False, False, 128),
+                                                   (2048, 4096, 256, False, True, True, 256),
+                                                   (4096, 2048, 64, True, True, False, 128),
+                                                   (4096, 2048, 4224, False, True, False, 128),
+                                                   (2048, 2048, 2048, False, False, False, 128),
+                                                   (2048, 2048, 1152, True, True, True, 128)])
+def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc, tile_m):
+    """Full tiles on the software-pipelined kernel. Grids of 512 128x128 tiles (16-deep
     slices): every operand layout ((K, MN), (MN, MN), (MN, K) and, with C column-major, the
     swapped product), alpha != 1 (fragments scaled as they are read) with beta != 0, K of one
-    pipeline step (64) and of several, and (K, K) operands with K >= 4096 (32-deep slices,
-    K = 4224: 132 slices). Grids of 256 tiles (one workgroup per compute unit, 32-deep
-    slices), also swapped. Against crates/cpu on every element; the same bits over two runs."""
+    pipeline step (64) and of several; those whose A-role operand is contiguous along K run as
+    256 tiles of 256x128 with eight waves (gemm_f32_pl256). (K, K) operands with K >= 4096
+    (32-deep slices, K = 4224: 132 slices). Grids of 256 tiles (one workgroup per compute
+    unit, 32-deep slices), also swapped. Against crates/cpu on every element; the same bits
+    over two runs."""
     pick = lambda t, r, c: Layout.transposed(r, c) if t else Layout.dense([r, c])
     la, lb, lc = pick(ta, m, k), pick(tb, k, n), pick(tc, m, n)
     g = rng(7700 + m + n + k)
@@ -966,7 +968,7 @@ def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc):
     Cc = Tensor.random(pool, lc, g)
     plan = C.plan_gemm(alpha, A.view(), B.view(), beta, Cc.view())
     assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"]) == \
-        ("pipelined", (128, 128), 1, m * n // (128 * 128)), plan
+        ("pipelined", (tile_m, 128), 1, m * n // (tile_m * 128)), plan
     c0 = Cc.host.copy()
     C.gemm(ctx, alpha, A.view(), B.view(), beta, Cc.view())
     first = Cc.read().copy()
