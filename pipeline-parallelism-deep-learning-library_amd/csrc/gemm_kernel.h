@@ -47,7 +47,9 @@ struct Geo {
 
 // Workgroup -> (plane, tile_m, tile_n). Workgroups are dealt round-robin to the 8 XCDs, so
 // the linear id is first regrouped so each XCD owns one contiguous run of tiles (sharing
-// its L2), then tiles within a plane are walked in groups of 8 tile-rows for A/B reuse.
+// its L2), then tiles within a plane are walked in groups of GROUP tile-rows for A/B reuse:
+// an XCD's resident tiles then cover GROUP tile-rows by a few tile-columns.
+template <uint32_t GROUP = 8>
 __device__ inline void decode_tile(uint32_t bid, uint32_t total, uint32_t tiles_m,
                                    uint32_t tiles_n, uint32_t* plane, uint32_t* tm,
                                    uint32_t* tn) {
@@ -57,7 +59,6 @@ __device__ inline void decode_tile(uint32_t bid, uint32_t total, uint32_t tiles_
     const uint32_t per_plane = tiles_m * tiles_n;
     *plane = lin / per_plane;
     const uint32_t t = lin - *plane * per_plane;
-    constexpr uint32_t GROUP = 8;
     const uint32_t group_size = GROUP * tiles_n;
     const uint32_t group = t / group_size;
     const uint32_t first_m = group * GROUP;

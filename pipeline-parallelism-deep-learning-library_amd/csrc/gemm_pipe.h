@@ -367,6 +367,10 @@ void gemm_f32_pl(GemmArgs p) {
 // B: it loads 3/4 of the operand bytes per FLOP that two 128x128 workgroups do. One workgroup
 // per compute unit (96 KiB of stages). Every K in whole steps of NS slices; M a multiple of 256,
 // N of 128; no split.
+// Tiles are walked in groups of PL256_GROUP tile-rows: an XCD's 32 resident tiles then form a
+// 4 x 8 block, 1024 x 1024 of C, which reads the fewest A rows plus B columns per round (traffic
+// below the L2 on 4096^3: 3.0x the algorithmic bytes, against 3.7x in groups of 8).
+constexpr uint32_t PL256_GROUP = 4;
 template <int AM, int BMD, int BK, int NS>
 __global__ __launch_bounds__(512, 1) void gemm_f32_pl256(GemmArgs p) {
     constexpr int FN = 2, RA = 256, RB = 128;
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(512, 1) void gemm_f32_pl256(GemmArgs p) {
     using GB = DlGeo<RB, BK, 512>;
     __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
     uint32_t plane, tm, tn;
-    decode_tile(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    decode_tile<PL256_GROUP>(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
     const uint32_t m0 = tm * RA, n0 = tn * RB;
     const float* A = p.a + static_cast<int64_t>(plane) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm;
     const float* B = p.b + static_cast<int64_t>(plane) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn;
