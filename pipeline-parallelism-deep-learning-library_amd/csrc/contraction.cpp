@@ -963,6 +963,23 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
         t.tiles_m = mm / PIPE_TALL_M;
         info.tile_m = PIPE_TALL_M;
     }
+    // Full 256x256 tiles, at least one per compute unit, whose A-role operand is contiguous
+    // along K take eight waves of 4x2 blocks (gemm_f32_pl2x, one workgroup per compute unit):
+    // per FLOP 2/3 of the operand loads of 256x128 tiles and 3/4 of their fragment reads
+    // (4096^3: 145 -> 148 TFLOP/s; config 3: 137 -> 142; config 5's dX, (K, K) with K = 16384,
+    // on them instead of 32-deep 128x128 slices).
+    if (t.kernel == KERN_PIPE && splits == 1 && a_mode == LOAD_K && b_mode != LOAD_S &&
+        mm % PIPE_TALL_M == 0 && nn % PIPE_WIDE_N == 0 && k % (PIPE_STAGES * 16) == 0 &&
+        (t.tile == PIPE_TALL_M || t.slice_k == 32) &&
+        static_cast<uint64_t>(mm / PIPE_TALL_M) * (nn / PIPE_WIDE_N) * batch >= GEMM_CUS) {
+        t.tile = PIPE_TALL_M;
+        t.tile_n = PIPE_WIDE_N;
+        t.tiles_m = mm / PIPE_TALL_M;
+        t.tiles_n = nn / PIPE_WIDE_N;
+        t.slice_k = 16;
+        info.tile_m = PIPE_TALL_M;
+        info.tile_n = PIPE_WIDE_N;
+    }
     // Stream-K: full 128x128 tiles, at least one per compute unit, that the grids above would
     // spread unevenly (the busiest compute unit more than 10/9 of the mean: the rank-4 48^6
     // product, 2304^3, has 324 tiles for 256 compute units) take gemm_f32_sk, which gives each

@@ -21,6 +21,7 @@ using gemm_detail::gemm_f32_mfma;
 using gemm_detail::gemm_f32_kw;
 using gemm_detail::gemm_f32_pl;
 using gemm_detail::gemm_f32_pl256;
+using gemm_detail::gemm_f32_pl2x;
 using gemm_detail::gemm_f32_sk;
 using gemm_detail::gemm_f32_small;
 using gemm_detail::gemm_f32_wave;
@@ -362,6 +363,18 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
                 return;
             }
             const uint32_t step = PIPE_STAGES * a.slice_k;
+            if (a.tile == PIPE_TALL_M && a.tile_n == PIPE_WIDE_N) {
+                if constexpr (AM == LOAD_K && BMD != LOAD_S) {
+                    if (a.m % PIPE_TALL_M != 0 || a.n % PIPE_WIDE_N != 0 || a.slice_k != 16 || a.splits != 1 ||
+                        a.k % step != 0) {
+                        fail_invalid("the 256x256 pipelined GEMM needs full tiles and K in whole steps");
+                    }
+                    hipLaunchKernelGGL((gemm_f32_pl2x<AM, BMD, 16, PIPE_STAGES>), dim3(groups), dim3(512), 0, s, a);
+                    return;
+                } else {
+                    fail_invalid("the 256x256 pipelined GEMM needs A contiguous along K");
+                }
+            }
             if (a.tile == PIPE_TALL_M) {
                 if (a.tile_n != GEMM_BN || a.m % PIPE_TALL_M != 0 || a.n % GEMM_BN != 0 || a.slice_k != 16 ||
                     a.splits != 1 || a.k % step != 0) {
@@ -478,7 +491,11 @@ void launch_gemm(Context* ctx, hipStream_t s, const GemmArgs& args, int a_mode, 
         {"gemm_f32_pl256<K,K>", "gemm_f32_pl256<K,MN>", "gemm_f32_pl256<K,S>"},
         {"gemm_f32_pl256<MN,K>", "gemm_f32_pl256<MN,MN>", "gemm_f32_pl256<MN,S>"},
         {"gemm_f32_pl256<S,K>", "gemm_f32_pl256<S,MN>", "gemm_f32_pl256<S,S>"}};
-    if (args.kernel == KERN_PIPE && args.tile == PIPE_TALL_M) {
+    if (args.kernel == KERN_PIPE && args.tile == PIPE_TALL_M && args.tile_n == PIPE_WIDE_N) {
+        name = a_mode != LOAD_K ? tall[a_mode][b_mode]
+               : b_mode == LOAD_K ? "gemm_f32_pl2x<K,K>"
+               : "gemm_f32_pl2x<K,MN>";
+    } else if (args.kernel == KERN_PIPE && args.tile == PIPE_TALL_M) {
         name = tall[a_mode][b_mode];
     } else if (args.kernel == KERN_PIPE && args.tile == GEMM_BM && args.tile_n == PIPE_NARROW_N) {
         name = narrow[a_mode][b_mode];

@@ -58,18 +58,22 @@ constexpr int pl_workgroups() {
     return by_lds < 3 ? by_lds : 3;
 }
 
-// The pipelined loop of one (64*WM) x (64*FN) output tile, WM x 2 waves of 2 x FN blocks (the
-// loop of gemm_f32_pl): `ktiles` slices of BK along K from A and B (pointers at the tile's first
-// row or column and its first k), added into acc. Leaves loads of the last slice in flight into
-// the LDS stages: a caller that reuses the stages waits for them.
-template <int AM, int BMD, int BK, int NS, int FN, int WM = 2>
+// The pipelined loop of one (32*FM*WM) x (32*FN*WN) output tile, WM x WN waves of FM x FN
+// blocks (the loop of gemm_f32_pl): `ktiles` slices of BK along K from A and B (pointers at the
+// tile's first row or column and its first k), added into acc. Leaves loads of the last slice in
+// flight into the LDS stages: a caller that reuses the stages waits for them. SPLIT issues a
+// slice's B loads in the last fragment group of the step that issues its A loads (past that
+// step's barrier, where the stage they fill is free as well) instead of beside them.
+template <int AM, int BMD, int BK, int NS, int FN, int WM = 2, int FM = 2, int WN = 2,
+          bool SPLIT = false>
 __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, const float* A,
                                              const float* B, uint32_t ktiles,
-                                             floatx16 (&acc)[2][FN]) {
+                                             floatx16 (&acc)[FM][FN]) {
     static_assert(AM != LOAD_S && BMD != LOAD_S, "direct loads need a unit-stride axis");
-    static_assert(FN == 1 || FN == 2, "64*WM x 64 or 64*WM x 128 tiles");
-    static_assert(WM == 2 || WM == 4, "WM x 2 waves of 2 x FN blocks");
-    constexpr int FM = 2, NW = 2 * WM, T = 64 * NW, RA = 32 * FM * WM, RB = 64 * FN;
+    static_assert(FN == 1 || FN == 2, "waves of FM x 1 or FM x 2 blocks");
+    static_assert(FM == 2 || FM == 4, "waves of 2 x FN or 4 x FN blocks");
+    static_assert(WM * WN == 4 || WM * WN == 8, "four or eight waves");
+    constexpr int NW = WM * WN, T = 64 * NW, RA = 32 * FM * WM, RB = 32 * FN * WN;
     using GA = DlGeo<RA, BK, T>;
     using GB = DlGeo<RB, BK, T>;
     constexpr int PER = GA::LOADS + GB::LOADS;  // load instructions per slice per thread
@@ -83,15 +87,25 @@ __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, con
     constexpr int RD = pl_reads<AM, BMD, FM, FN>();
     constexpr int RPM = RD > MG * 3 / 4 ? 2 : 1;
     constexpr int RM = (RD + RPM - 1) / RPM;
-    constexpr int NV = (PER + 1) / 2;
+    constexpr int NV = ((SPLIT ? GA::LOADS : PER) + 1) / 2;
+    constexpr int NVB = SPLIT ? (GB::LOADS + 1) / 2 : 0;
+    // Loads issued after slice kt + 1's last one when step kt reaches its barrier.
+    constexpr int AFTER = SPLIT ? (NS - 3) * PER + GA::LOADS : (NS - 2) * PER;
+    static_assert(!SPLIT || NS >= 3, "split loads keep two slices ahead");
     constexpr int VF0 = 10 - RM < MG - RM - NV ? 10 - RM : MG - RM - NV;
     constexpr int VF = VF0 > 0 ? VF0 : 0;
     static_assert(RM + VF + NV <= MG, "MFMAs of a group");
 
     float* As = smem;
-    float* Bs = smem + NS * GA::ST;
+    // The B stages start past the A stages. Where that start is beyond the 64 KiB reach of a
+    // DS instruction's offset, the compiler, folding it into every read, holds one address
+    // register per B fragment read; hidden from it (an empty asm), every read is one register
+    // plus an offset.
+    uint32_t b_first = NS * GA::ST;
+    if constexpr (FM == 4) __asm__ volatile("" : "+s"(b_first));
+    float* Bs = smem + b_first;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WN, wn = wave % WN;
     const int lr = lane & 31, h = lane >> 5;
 
     const float alpha_a = p.scale_b ? 1.0f : p.alpha;
@@ -105,13 +119,19 @@ __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, con
     const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
     const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
     // Slice kt into `stage`.
-    auto issue = [&](uint32_t kt, int stage) {
+    auto issue_a = [&](uint32_t kt, int stage) {
         float* as = As + stage * GA::ST;
-        float* bs = Bs + stage * GB::ST;
 #pragma unroll
         for (int i = 0; i < GA::LOADS; ++i) dl_copy16(A + sa[i] + kt * a_step, as + (i * NW + wave) * 256);
+    };
+    auto issue_b = [&](uint32_t kt, int stage) {
+        float* bs = Bs + stage * GB::ST;
 #pragma unroll
         for (int i = 0; i < GB::LOADS; ++i) dl_copy16(B + sb[i] + kt * b_step, bs + (i * NW + wave) * 256);
+    };
+    auto issue = [&](uint32_t kt, int stage) {
+        issue_a(kt, stage);
+        issue_b(kt, stage);
     };
 
     auto run = [&](auto scale) {
@@ -143,7 +163,13 @@ __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, con
 #pragma unroll
                 for (int g = 0; g + 1 < G; ++g) {
                     read((g + 1) & 1, g + 1, u);
-                    if (g == 0) issue(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                    if (g == 0) {
+                        if constexpr (SPLIT) {
+                            issue_a(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                        } else {
+                            issue(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                        }
+                    }
                     mfma_group<FM, FN>(acc, fa[g & 1], fb[g & 1]);
                     pl_after_each_mfma<RM, 0x100, RPM>();
                     if (g == 0) {
@@ -156,14 +182,20 @@ __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, con
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // Slice kt + 1 landed for every wave, slice kt read by every wave.
-                wait_vm<(NS - 2) * PER>();
+                wait_vm<AFTER>();
                 wait_lgkm0();
                 __builtin_amdgcn_s_barrier();
                 constexpr int L = (G - 1) & 1;
                 read(0, 0, (u + 1) % NS);  // past the last slice: unused
+                if constexpr (SPLIT) issue_b(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
                 mfma_group<FM, FN>(acc, fa[L], fb[L]);
                 pl_after_each_mfma<RM, 0x100, RPM>();
-                __builtin_amdgcn_sched_group_barrier(0x008, MG - RM, 0);
+                if constexpr (SPLIT) {
+                    pl_after_each_mfma<NVB, 0x010, 2>();
+                    __builtin_amdgcn_sched_group_barrier(0x008, MG - RM - NVB, 0);
+                } else {
+                    __builtin_amdgcn_sched_group_barrier(0x008, MG - RM, 0);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -176,14 +208,13 @@ __device__ __forceinline__ void pl_tile_loop(const GemmArgs& p, float* smem, con
 
 }
 
-// Stores one 128 x 64*FN tile of C (plane bi, first row m0, first column n0): beta * C + acc,
-// or acc alone when beta is 0 (C never read).
-template <int FN>
-__device__ __forceinline__ void pl_store_c(const GemmArgs& p, const floatx16 (&acc)[2][FN],
+// Stores one tile of C of waves in WN columns with FM x FN blocks each (plane bi, first row m0,
+// first column n0): beta * C + acc, or acc alone when beta is 0 (C never read).
+template <int FN, int FM = 2, int WN = 2>
+__device__ __forceinline__ void pl_store_c(const GemmArgs& p, const floatx16 (&acc)[FM][FN],
                                            uint32_t bi, uint32_t m0, uint32_t n0) {
-    constexpr int FM = 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WN, wn = wave % WN;
     const int lr = lane & 31, h = lane >> 5;
     float* C = p.c + static_cast<int64_t>(bi) * p.c_sb;
 #pragma unroll
@@ -391,6 +422,35 @@ __global__ __launch_bounds__(512, 1) void gemm_f32_pl256(GemmArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     pl_tile_loop<AM, BMD, BK, NS, FN, 4>(p, smem, A, B, p.k / BK, acc);
     pl_store_c<FN>(p, acc, plane, m0, n0);
+}
+
+// gemm_f32_pl2x<AM, BMD, BK, NS>: the pipelined loop on full 256x256 tiles with eight waves (2x4,
+// each 4x2 blocks of 32x32: 128 x 64 of C, 128 accumulators), two per SIMD, one workgroup per
+// compute unit (128 KiB of stages): per FLOP 2/3 of the operand loads of the 256x128 tiles and
+// 3/4 of their fragment reads. With B contiguous along N (each wave instruction a 1 KiB k-row
+// of B) a slice's B loads go out in the step's last fragment group, apart from its A loads:
+// issued together they held 4096^3 at 134 TFLOP/s, apart 148. Every K in whole steps of NS
+// slices; M and N multiples of 256; no split.
+template <int AM, int BMD, int BK, int NS>
+__global__ __launch_bounds__(512, 1) void gemm_f32_pl2x(GemmArgs p) {
+    constexpr int FM = 4, FN = 2, WM = 2, WN = 4, RA = 256, RB = 256;
+    using GA = DlGeo<RA, BK, 512>;
+    using GB = DlGeo<RB, BK, 512>;
+    __shared__ __attribute__((aligned(16))) float smem[NS * (GA::ST + GB::ST)];
+    uint32_t plane, tm, tn;
+    decode_tile<PL256_GROUP>(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, &plane, &tm, &tn);
+    const uint32_t m0 = tm * RA, n0 = tn * RB;
+    const float* A = p.a + static_cast<int64_t>(plane) * p.a_sb + static_cast<int64_t>(m0) * p.a_sm;
+    const float* B = p.b + static_cast<int64_t>(plane) * p.b_sb + static_cast<int64_t>(n0) * p.b_sn;
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    pl_tile_loop<AM, BMD, BK, NS, FN, WM, FM, WN, BMD == LOAD_MN>(p, smem, A, B, p.k / BK, acc);
+    pl_store_c<FN, FM, WN>(p, acc, plane, m0, n0);
 }
 
 // gemm_f32_sk<AM, BMD, BK, NS>: stream-K over the pipelined loop of full 128x128 tiles. The T

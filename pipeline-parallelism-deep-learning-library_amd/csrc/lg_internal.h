@@ -153,6 +153,7 @@ constexpr uint32_t PIPE_STAGES = 4;
 constexpr uint32_t PIPE_KW = 4;  // waves splitting K on 64x64 tiles
 constexpr uint32_t PIPE_NARROW_N = 64;  // N extent of the 128x64 pipelined tile
 constexpr uint32_t PIPE_TALL_M = 256;   // M extent of the 256x128 pipelined tile (gemm_f32_pl256)
+constexpr uint32_t PIPE_WIDE_N = 256;   // N extent of the 256x256 pipelined tile (gemm_f32_pl2x)
 constexpr uint32_t PIPE_DEEP_K = 4096;  // (K, K) chunks from this long take 32-deep slices
 constexpr uint32_t OUTER_MAX_K = 8;
 

@@ -331,10 +331,17 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     for m, n, k in [(2048, 2048, 1936), (2040, 2048, 2048)]:
         p = C.plan_gemm(1.0, dense([m, k]), dense([k, n]), 0.0, dense([m, n]))
         assert (p["kind"], p["kernel"], p["tile"], p["kgroups"]) == ("tiled", "direct", (128, 128), 2)
-    # 4096^3: 1024 128x128 pipelined tiles with A contiguous along K pair up into 512 256x128
-    # tiles of eight waves (one workgroup per compute unit, two waves per SIMD).
+    # 4096^3: 1024 128x128 pipelined tiles with A contiguous along K merge into 256 256x256
+    # tiles of eight waves (one workgroup per compute unit, two waves per SIMD), B contiguous
+    # along N or along K.
     p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 4096]), 0.0, dense([4096, 4096]))
-    assert (p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == ("pipelined", (256, 128), 1, 512)
+    assert (p["kernel"], p["tile"], p["kgroups"], p["workgroups"]) == ("pipelined", (256, 256), 1, 256)
+    Bt = view(Layout.transposed(4096, 4096))
+    p = C.plan_gemm(1.0, dense([4096, 4096]), Bt, 0.0, dense([4096, 4096]))
+    assert (p["kernel"], p["tile"], p["b_mode"], p["workgroups"]) == ("pipelined", (256, 256), "k", 256)
+    # Fewer than 256 of them (4096 x 2048: 128): 256x128 tiles, 256 of those.
+    p = C.plan_gemm(1.0, dense([4096, 4096]), dense([4096, 2048]), 0.0, dense([4096, 2048]))
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (256, 128), 256)
     # A contiguous along M keeps 128x128 tiles.
     p = C.plan_gemm(1.0, view(Layout.transposed(4096, 4096)), dense([4096, 4096]), 0.0, dense([4096, 4096]))
     assert (p["kernel"], p["tile"], p["a_mode"], p["workgroups"]) == ("pipelined", (128, 128), "mn", 1024)
@@ -361,8 +368,8 @@ def test_contraction_plans_for_the_baseline_configs():
     p = C.plan_contract(1.0, (dense([32, 1024, 1024]), "bik"), (bview, "bkj"), 0.0,
                         (dense([32, 1024, 1024]), "bij"))
     assert p["kind"] == "tiled" and p["batch"] == 32 and p["b_mode"] == "k" and p["a_mode"] == "k"
-    # 2048 full 128x128 tiles: the pipelined kernel, as 1024 256x128 tiles of eight waves.
-    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (256, 128), 32 * 4 * 8)
+    # 2048 full 128x128 tiles: the pipelined kernel, as 512 256x256 tiles of eight waves.
+    assert (p["kernel"], p["tile"], p["workgroups"]) == ("pipelined", (256, 256), 32 * 4 * 4)
     # Config 4: tall K goes split-K with a fixed chunk grid.
     p = C.plan_gemm(1.0, dense([256, 65536]), dense([65536, 256]), 0.0, dense([256, 256]))
     assert p["kind"] == "split" and p["splits"] > 1 and p["k_chunk"] % 32 == 0
@@ -382,9 +389,10 @@ def test_contraction_plans_for_the_baseline_configs():
     Wt = L.TensorView(W.buffer, 0, [16384, 4096], [1, 16384])
     Xt = L.TensorView(X.buffer, 0, [4096, 4096], [1, 4096])
     p = C.plan_gemm(1.0, X, W, 0.0, dense([4096, 16384]))
-    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "pipelined", (256, 128), 16 * 128)
+    assert (p["kind"], p["kernel"], p["tile"], p["workgroups"]) == ("tiled", "pipelined", (256, 256), 16 * 64)
     p = C.plan_gemm(1.0, dY, Wt, 0.0, dense([4096, 4096]))
-    assert (p["a_mode"], p["b_mode"], p["kernel"]) == ("k", "k", "pipelined")
+    assert (p["a_mode"], p["b_mode"], p["kernel"], p["tile"], p["workgroups"]) == \
+        ("k", "k", "pipelined", (256, 256), 256)
     p = C.plan_gemm(1.0, Xt, dY, 1.0, dense([4096, 16384]))
     assert (p["a_mode"], p["b_mode"], p["kernel"]) == ("mn", "mn", "pipelined")
 

@@ -978,3 +978,44 @@ def test_pipelined_kernel(ctx, pool, m, n, k, ta, tb, tc, tile_m):
     assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
     _gemm_fast_check(f"pipelined {m}x{n}x{k} ta={ta} tb={tb} tc={tc}", first, A.host, la,
                      B.host, lb, c0, lc, m, n, k, alpha, beta)
+
+
+@pytest.mark.parametrize("m,n,k,tc,batch,bk,ab", [(4096, 4096, 512, False, 1, True, False),
+                                                  (4096, 4096, 1088, True, 1, True, True),
+                                                  (1024, 1024, 256, False, 16, True, False),
+                                                  (4096, 4096, 4160, False, 1, True, False),
+                                                  (4096, 4096, 320, False, 1, False, False),
+                                                  (4096, 4096, 1088, False, 1, False, True),
+                                                  (1024, 1024, 256, False, 16, False, True)])
+def test_pipelined_256x256_tiles(ctx, pool, m, n, k, tc, batch, bk, ab):
+    """A row-major with B transposed (K, K) or row-major (K, MN, whose B loads go out apart from
+    the A loads), 256x256 tiles numbering at least one per compute unit: gemm_f32_pl2x (eight
+    waves of 4x2 blocks). 256 tiles; with C column-major (the swapped product, K = 1088: 17
+    pipeline steps); 16 batches of 16 tiles; K = 4160 (65 steps), which 128x128 tiles would take
+    on 32-deep slices; alpha != 1 with beta != 0 where marked. Against crates/cpu on every
+    element of every batch; the same bits over two runs."""
+    la = Layout(0, [batch, m, k], [m * k, k, 1])
+    lb = Layout(0, [batch, k, n], [k * n, 1, k] if bk else [k * n, n, 1])
+    lc = Layout(0, [batch, m, n], [m * n, 1, m] if tc else [m * n, n, 1])
+    g = rng(7750 + m + k + batch + 2 * bk)
+    alpha, beta = (0.75, -0.5) if ab else (1.0, 0.0)
+    A, B, Cc = Tensor.random(pool, la, g), Tensor.random(pool, lb, g), Tensor.random(pool, lc, g)
+    if batch == 1:  # plain matrices: the same buffers as rank-2 views
+        mat = lambda t_: L.TensorView(t_.buffer, 0, t_.layout.shape[1:], t_.layout.strides[1:])
+        av, bv, cv = mat(A), mat(B), mat(Cc)
+    else:
+        av, bv, cv = A.view(), B.view(), Cc.view()
+    plan = C.plan_gemm(alpha, av, bv, beta, cv)
+    assert (plan["kernel"], plan["tile"], plan["kgroups"], plan["workgroups"], plan["b_mode"]) == \
+        ("pipelined", (256, 256), 1, batch * m * n // 65536, "k" if bk else "mn"), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, alpha, av, bv, beta, cv)
+    first = Cc.read().copy()
+    Cc.host[:] = c0
+    Cc.upload()
+    C.gemm(ctx, alpha, av, bv, beta, cv)
+    assert np.array_equal(first.view(np.uint32), Cc.read().view(np.uint32))
+    for i in range(batch):
+        at = lambda lay: Layout(i * lay.strides[0], lay.shape[1:], lay.strides[1:])
+        _gemm_fast_check(f"256x256 {m}x{n}x{k} tc={tc} bk={bk} batch {i}", first, A.host, at(la),
+                         B.host, at(lb), c0, at(lc), m, n, k, alpha, beta)
