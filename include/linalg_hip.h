@@ -406,7 +406,9 @@ typedef enum lg_plan_kernel {
     LG_KERNEL_DOT = 4,   /* one dot product (chunk) per workgroup */
     LG_KERNEL_OUTER = 5, /* K <= 8: four outputs per thread on the VALU, summed in k order */
     LG_KERNEL_DIRECT = 6, /* 128x128 or 128x256 tile, operand slices loaded straight into LDS */
-    LG_KERNEL_PIPELINED = 7, /* full 128x128 tiles, direct loads, software-pipelined waves */
+    LG_KERNEL_PIPELINED = 7, /* full tiles, direct loads, software-pipelined waves: 128x128,
+                                128x64, 64x64 (K split over the waves), and with A contiguous
+                                along K 256x128 or 256x256 tiles of eight waves */
     LG_KERNEL_STREAMK = 8   /* full 128x128 tiles spread unevenly over the compute units: one
                                workgroup per compute unit takes an equal run of the pipelined
                                kernel's K steps across tiles; a tile two runs share is summed by
@@ -431,7 +433,9 @@ typedef struct lg_contract_plan {
     uint64_t workgroups;  /* workgroups of the main launch */
     uint64_t scratch_bytes; /* device scratch of the split-K partials */
     uint32_t tile_m;      /* output tile of one workgroup or wave (tiled/split): 128x128 on */
-    uint32_t tile_n;      /* the pipelined kernel (full tiles, at least 512 workgroups), else
+    uint32_t tile_n;      /* the pipelined kernel (full tiles, at least 512 workgroups; with A
+                             contiguous along K 256x128, or 256x256 where at least 256 of
+                             those fill the output), else
                              128x256 for grids of at least 512 such tiles, else 128x128; 64x64
                              when 128x128 tiles would leave most compute units idle or be
                              mostly padding;
