@@ -611,8 +611,8 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
     constexpr int RPM = RD > 12 ? 2 : 1;
     constexpr int RM = (RD + RPM - 1) / RPM;
     constexpr int VF = RM < 10 ? 10 - RM : 0;
-    constexpr int VPM = PER / 4;  // loads after each of four MFMAs
-    static_assert(RM + VF + 4 <= 16, "a group has 16 MFMAs");
+    constexpr int VPM = PER / 4;  // loads after each of two MFMAs (A or B: half the slice)
+    static_assert(RM + VF + 2 <= 16, "a group has 16 MFMAs");
     constexpr int WST = NS * (GA::ST + GB::ST);
     static_assert(W * WST >= W * FM * FN * 16 * 64, "the sums fit in the stages");
     __shared__ __attribute__((aligned(16))) float smem[W * WST];
@@ -643,14 +643,26 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
     for (int i = 0; i < GB::LOADS; ++i) sb[i] = dl_src<BMD, R, BK>(i * 64 + lane, p.b_sn, p.b_sk);
     const int64_t a_step = AM == LOAD_K ? BK : static_cast<int64_t>(BK) * p.a_sk;
     const int64_t b_step = BMD == LOAD_K ? BK : static_cast<int64_t>(BK) * p.b_sk;
-    auto issue = [&](uint32_t kt, int stage) {
+    // A slice's A loads go out in the first fragment group of the step three slices ahead of
+    // it, its B loads in that step's last group (1024^3: 98-99 -> 101.5 TFLOP/s, config 4
+    // 114-115 -> 117-120 against all eight together in the first group).
+    auto issue_a = [&](uint32_t kt, int stage) {
         float* as = As + stage * GA::ST;
-        float* bs = Bs + stage * GB::ST;
 #pragma unroll
         for (int i = 0; i < GA::LOADS; ++i) dl_copy16(A + sa[i] + kt * a_step, as + i * 256);
+    };
+    auto issue_b = [&](uint32_t kt, int stage) {
+        float* bs = Bs + stage * GB::ST;
 #pragma unroll
         for (int i = 0; i < GB::LOADS; ++i) dl_copy16(B + sb[i] + kt * b_step, bs + i * 256);
     };
+    auto issue = [&](uint32_t kt, int stage) {
+        issue_a(kt, stage);
+        issue_b(kt, stage);
+    };
+    // Loads issued after slice kt + 1's last one when step kt waits for it.
+    constexpr int AFTER = (NS - 3) * PER + GA::LOADS;
+    static_assert(NS >= 3, "A and B loads of a slice go out in different steps' groups");
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -684,24 +696,26 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
 #pragma unroll
                 for (int g = 0; g + 1 < G; ++g) {
                     read((g + 1) & 1, g + 1, u);
-                    if (g == 0) issue(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                    if (g == 0) issue_a(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
                     mfma_group<FM, FN>(acc, fa[g & 1], fb[g & 1]);
                     pl_after_each_mfma<RM, 0x100, RPM>();
                     if (g == 0) {
                         if constexpr (VF > 0) __builtin_amdgcn_sched_group_barrier(0x008, VF, 0);
-                        pl_after_each_mfma<4, 0x010, VPM>();
-                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - VF - 4, 0);
+                        pl_after_each_mfma<2, 0x010, VPM>();
+                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - VF - 2, 0);
                     } else {
                         __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                wait_vm<(NS - 2) * PER>();  // slice kt + 1 landed (this wave's own loads)
+                wait_vm<AFTER>();  // slice kt + 1 landed (this wave's own loads)
                 constexpr int L = (G - 1) & 1;
                 read(0, 0, (u + 1) % NS);
+                issue_b(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
                 mfma_group<FM, FN>(acc, fa[L], fb[L]);
                 pl_after_each_mfma<RM, 0x100, RPM>();
-                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
+                pl_after_each_mfma<2, 0x010, VPM>();
+                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - 2, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
