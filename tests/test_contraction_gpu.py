@@ -992,14 +992,18 @@ def test_pipelined_256x256_tiles(ctx, pool, m, n, k, tc, batch, bk, ab):
     the A loads), 256x256 tiles numbering at least one per compute unit: gemm_f32_pl2x (eight
     waves of 4x2 blocks). 256 tiles; with C column-major (the swapped product, K = 1088: 17
     pipeline steps); 16 batches of 16 tiles; K = 4160 (65 steps), which 128x128 tiles would take
-    on 32-deep slices; alpha != 1 with beta != 0 where marked. Against crates/cpu on every
-    element of every batch; the same bits over two runs."""
+    on 32-deep slices; alpha != 1 with beta != 0 where marked, else C filled with NaN (beta = 0
+    never reads it). Against crates/cpu on every element of every batch; the same bits over
+    two runs."""
     la = Layout(0, [batch, m, k], [m * k, k, 1])
     lb = Layout(0, [batch, k, n], [k * n, 1, k] if bk else [k * n, n, 1])
     lc = Layout(0, [batch, m, n], [m * n, 1, m] if tc else [m * n, n, 1])
     g = rng(7750 + m + k + batch + 2 * bk)
     alpha, beta = (0.75, -0.5) if ab else (1.0, 0.0)
     A, B, Cc = Tensor.random(pool, la, g), Tensor.random(pool, lb, g), Tensor.random(pool, lc, g)
+    if beta == 0.0:  # C must never be read: NaN there would reach the result
+        Cc.host[:] = np.nan
+        Cc.upload()
     if batch == 1:  # plain matrices: the same buffers as rank-2 views
         mat = lambda t_: L.TensorView(t_.buffer, 0, t_.layout.shape[1:], t_.layout.strides[1:])
         av, bv, cv = mat(A), mat(B), mat(Cc)
