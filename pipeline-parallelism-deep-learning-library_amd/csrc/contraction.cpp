@@ -1061,6 +1061,67 @@ Plan plan_gemm(float alpha, const lg_view* a_c, const lg_view* b_c, float beta, 
     return plan_merged(*a, *b, *c, merge_all(groups_from_gemm(*a, *b, *c)), alpha, beta, half);
 }
 
+// Plans of the last few gemm calls on this thread, keyed on every input the planner reads: the
+// three views' fields, alpha and beta as bits and the element width. A call repeating one of
+// them (the same views again, as a training loop or a benchmark makes) skips the planner's
+// work, about 1 us of host time against a few us per launch; a plan is a function of exactly
+// these inputs, so a hit returns what planning would. Inputs the planner rejects are never
+// stored, so they are rejected again.
+struct CachedPlan {
+    bool used = false;
+    bool half = false;
+    uint32_t alpha_bits = 0, beta_bits = 0;
+    lg_view v[3];
+    Plan plan;
+};
+constexpr int PLAN_CACHE = 4;
+thread_local CachedPlan plan_cache[PLAN_CACHE];
+thread_local int plan_cache_next = 0;
+
+bool cacheable(const lg_view* v) {
+    return v != nullptr && v->rank <= LG_MAX_RANK && v->nstrides <= LG_MAX_RANK;
+}
+bool same_view(const lg_view& x, const lg_view* y) {
+    if (x.base != y->base || x.bytes != y->bytes || x.offset != y->offset || x.rank != y->rank ||
+        x.nstrides != y->nstrides) {
+        return false;
+    }
+    for (uint32_t i = 0; i < x.rank; ++i) {
+        if (x.shape[i] != y->shape[i]) return false;
+    }
+    for (uint32_t i = 0; i < x.nstrides; ++i) {
+        if (x.strides[i] != y->strides[i]) return false;
+    }
+    return true;
+}
+
+Plan plan_gemm_cached(float alpha, const lg_view* a, const lg_view* b, float beta, const lg_view* c,
+                      bool half = false) {
+    View va, vb, vc;
+    if (!cacheable(a) || !cacheable(b) || !cacheable(c)) return plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc, half);
+    uint32_t ab, bb;
+    std::memcpy(&ab, &alpha, 4);
+    std::memcpy(&bb, &beta, 4);
+    for (const CachedPlan& e : plan_cache) {
+        if (e.used && e.half == half && e.alpha_bits == ab && e.beta_bits == bb && same_view(e.v[0], a) &&
+            same_view(e.v[1], b) && same_view(e.v[2], c)) {
+            return e.plan;
+        }
+    }
+    Plan p = plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc, half);
+    CachedPlan& e = plan_cache[plan_cache_next];
+    plan_cache_next = (plan_cache_next + 1) % PLAN_CACHE;
+    e.used = true;
+    e.half = half;
+    e.alpha_bits = ab;
+    e.beta_bits = bb;
+    e.v[0] = *a;
+    e.v[1] = *b;
+    e.v[2] = *c;
+    e.plan = p;
+    return p;
+}
+
 // Device scratch handed to a split or split-dot plan's launches: the partials.
 struct Scratch {
     float* partial = nullptr;
@@ -1233,8 +1294,7 @@ lg_status lg_encode_gemm_f32(lg_ctx* ctx, void* stream, float alpha, const lg_vi
                              const lg_view* b, float beta, const lg_view* c) {
     return guarded([&] {
         if (ctx == nullptr) fail_invalid("null context");
-        View va, vb, vc;
-        run(ctx, stream, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc), false);
+        run(ctx, stream, plan_gemm_cached(alpha, a, b, beta, c), false);
     });
 }
 
@@ -1242,8 +1302,7 @@ lg_status lg_gemm_f32(lg_ctx* ctx, float alpha, const lg_view* a, const lg_view*
                       const lg_view* c) {
     return guarded([&] {
         if (ctx == nullptr) fail_invalid("null context");
-        View va, vb, vc;
-        run(ctx, nullptr, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc), true);
+        run(ctx, nullptr, plan_gemm_cached(alpha, a, b, beta, c), true);
     });
 }
 
@@ -1251,8 +1310,7 @@ lg_status lg_gemm_nowait_f32(lg_ctx* ctx, float alpha, const lg_view* a, const l
                              float beta, const lg_view* c) {
     return guarded([&] {
         if (ctx == nullptr) fail_invalid("null context");
-        View va, vb, vc;
-        run(ctx, nullptr, plan_gemm(alpha, a, b, beta, c, &va, &vb, &vc), false);
+        run(ctx, nullptr, plan_gemm_cached(alpha, a, b, beta, c), false);
     });
 }
 

@@ -256,6 +256,51 @@ def test_in_place_scale(ctx, pool):
     oracle.gate(got, e, "in-place row scale")
 
 
+def test_repeated_calls_plan_again_on_any_change(ctx, pool):
+    """The library keeps the plans of a thread's last few gemm calls, keyed on the views,
+    alpha and beta. A repeat gives the same bits; the same shapes on other buffers, another
+    beta, a shifted offset or an overlapping destination are planned again (the overlap still
+    rejected, nothing launched), and the first call afterwards still holds."""
+    m, n, k = 256, 192, 320
+    g = rng(1750)
+    A1, A2 = (Tensor.random(pool, Layout.dense([m, k]), g) for _ in range(2))
+    B1, B2 = (Tensor.random(pool, Layout.dense([k, n]), g) for _ in range(2))
+    C1, C2 = (Tensor.random(pool, Layout.dense([m, n]), g) for _ in range(2))
+    c1_0, c2_0 = C1.host.copy(), C2.host.copy()
+
+    def check(name, Cc, c0, A, B, alpha, beta, la=Layout.dense([m, k])):
+        _gemm_fast_check(name, Cc.read(), A.host, la, B.host, Layout.dense([k, n]), c0,
+                         Layout.dense([m, n]), m, n, k, alpha, beta)
+
+    C.gemm(ctx, 1.0, A1.view(), B1.view(), 0.0, C1.view())
+    first = C1.read().copy()
+    check("first call", C1, c1_0, A1, B1, 1.0, 0.0)
+    C.gemm(ctx, 1.0, A1.view(), B1.view(), 0.0, C1.view())
+    assert np.array_equal(first.view(np.uint32), C1.read().view(np.uint32))
+    # Same shapes, other buffers: C2 written, C1 untouched.
+    C.gemm(ctx, 1.0, A2.view(), B2.view(), 0.0, C2.view())
+    check("other buffers", C2, c2_0, A2, B2, 1.0, 0.0)
+    assert np.array_equal(first.view(np.uint32), C1.read().view(np.uint32))
+    # Same views, another beta (C2 now holds A2.B2).
+    c2_1 = C2.read().copy()
+    C.gemm(ctx, 1.0, A1.view(), B1.view(), 0.5, C2.view())
+    check("beta 0.5", C2, c2_1, A1, B1, 1.0, 0.5)
+    # A view shifted by one element (the last row of A2's buffer, its spare tail, unread before).
+    shifted = L.TensorView(A2.buffer, 1, [m, k], [k, 1])
+    c2_2 = C2.read().copy()
+    C.gemm(ctx, -0.75, shifted, B1.view(), 0.0, C2.view())
+    check("shifted A", C2, c2_2, A2, B1, -0.75, 0.0, la=Layout(1, [m, k], [k, 1]))
+    # A destination overlapping A, shapes unchanged: rejected before any launch.
+    n0 = ctx.launches()
+    over = L.TensorView(A1.buffer, 0, [m, n], [n, 1])
+    with pytest.raises(L.Overlap):
+        C.gemm(ctx, 1.0, A1.view(), B1.view(), 0.0, over)
+    assert ctx.launches() == n0
+    assert np.array_equal(A1.read().view(np.uint32), A1.host.view(np.uint32))
+    C.gemm(ctx, 1.0, A1.view(), B1.view(), 0.0, C1.view())
+    assert np.array_equal(first.view(np.uint32), C1.read().view(np.uint32))
+
+
 def test_overlap_rejected_without_launch(ctx, pool):
     n = 24
     g = rng(1800)
