@@ -286,7 +286,7 @@ def test_contraction_plans_for_the_reference_benchmark_shapes():
     p = C.plan_contract(1.0, (dense([4096, 1]), "mk"), (dense([1, 4096]), "kn"), 0.0,
                         (dense([4096, 4096]), "mn"))
     assert (p["kind"], p["kernel"], p["tile"], p["b_mode"]) == ("tiled", "outer", (1, 4), "mn")
-    assert p["workgroups"] == 2048  # a grid-stride loop over the 4096 * 1024 quads
+    assert p["workgroups"] == 4096  # a grid-stride loop over the 4096 * 1024 quads
     p = C.plan_contract(1.0, (dense([48] * 4), "ijkl"), (dense([48] * 4), "klmn"), 0.0,
                         (dense([48] * 4), "ijmn"))
     assert (p["kind"], p["groups"], p["m"], p["n"], p["k"]) == ("tiled", 1, 2304, 2304, 2304)
