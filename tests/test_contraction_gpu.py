@@ -1068,3 +1068,28 @@ def test_pipelined_256x256_tiles(ctx, pool, m, n, k, tc, batch, bk, ab):
         at = lambda lay: Layout(i * lay.strides[0], lay.shape[1:], lay.strides[1:])
         _gemm_fast_check(f"256x256 {m}x{n}x{k} tc={tc} bk={bk} batch {i}", first, A.host, at(la),
                          B.host, at(lb), c0, at(lc), m, n, k, alpha, beta)
+
+
+@pytest.mark.parametrize("bk", [True, False])
+def test_pipelined_256x256_tiles_offset_padded_views(ctx, pool, bk):
+    """The 256x256 tiles read and write through view offsets and padded row pitches (each a
+    multiple of four elements, so 128-bit loads stay aligned): A at offset 8 with rows of
+    K + 4, B (transposed, or row-major) at offset 4 with a pitch of 4 more, C at offset 12 with
+    rows of N + 8, alpha != 1 and beta != 0; every element against crates/cpu, the padding
+    left untouched."""
+    m, n, k = 4096, 4096, 256
+    la = Layout(8, [m, k], [k + 4, 1])
+    lb = Layout(4, [k, n], [1, k + 4]) if bk else Layout(4, [k, n], [n + 4, 1])
+    lc = Layout(12, [m, n], [n + 8, 1])
+    g = rng(7990 + bk)
+    A, B, Cc = Tensor.random(pool, la, g), Tensor.random(pool, lb, g), Tensor.random(pool, lc, g)
+    plan = C.plan_gemm(0.75, A.view(), B.view(), -0.5, Cc.view())
+    assert (plan["kernel"], plan["tile"], plan["workgroups"], plan["b_mode"]) == \
+        ("pipelined", (256, 256), 256, "k" if bk else "mn"), plan
+    c0 = Cc.host.copy()
+    C.gemm(ctx, 0.75, A.view(), B.view(), -0.5, Cc.view())
+    got = Cc.read()
+    written = (lc.offset + np.arange(m)[:, None] * lc.strides[0] + np.arange(n)[None, :]).ravel()
+    assert_untouched("256x256 padded C", c0, got, written)
+    _gemm_fast_check(f"256x256 offset views bk={bk}", got, A.host, la, B.host, lb, c0, lc, m, n, k,
+                     0.75, -0.5)
