@@ -891,9 +891,9 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     // with a quarter of K each, no barrier in the loop (1024^3: 75 -> 97-99 TFLOP/s).
     const bool full64 = mm % GEMM_SMALL_TILE == 0 && nn % GEMM_SMALL_TILE == 0;
     if (t.kernel == KERN_DIRECT && t.tile == GEMM_SMALL_TILE && t.kgroups == 4 && full64 &&
-        chunk % (PIPE_KW * PIPE_STAGES * 16) == 0 && last_chunk % (PIPE_KW * PIPE_STAGES * 16) == 0) {
+        chunk % KW_STEP == 0 && last_chunk % KW_STEP == 0) {
         t.kernel = KERN_PIPE;
-        t.slice_k = 16;
+        t.slice_k = KW_BK;
     }
     if (t.kernel == KERN_DIRECT && t.tile == GEMM_BM && full) {
         if (t.kgroups == 1 && tiles128 >= 2 * GEMM_CUS && whole(16)) {
@@ -933,7 +933,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     // K-split-wave kernel on 64x64 tiles instead, split to about one workgroup per compute unit
     // in chunks of whole steps: fewer, longer splits (config 4: 16 of 4096 instead of 128 of
     // 512 on 128x128 tiles, 4 MiB of partials instead of 32; 112 -> 116 TFLOP/s).
-    const uint32_t kw_step = PIPE_KW * PIPE_STAGES * 16;
+    const uint32_t kw_step = KW_STEP;
     if (t.kernel == KERN_PIPE && t.tile == GEMM_BM && splits > 1 && full64 && k % kw_step == 0) {
         const uint64_t t64 = static_cast<uint64_t>(mm / GEMM_SMALL_TILE) * (nn / GEMM_SMALL_TILE) * batch;
         if (t64 <= GEMM_CUS / 2) {
@@ -948,7 +948,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
                 splits = static_cast<uint32_t>(s64);
                 chunk = static_cast<uint32_t>(c64);
                 t.kgroups = PIPE_KW;
-                t.slice_k = 16;
+                t.slice_k = KW_BK;
             }
         }
     }
@@ -970,7 +970,7 @@ Plan plan_merged(const View& a, const View& b, const View& c, const Merged& mg, 
     // on them instead of 32-deep 128x128 slices).
     if (t.kernel == KERN_PIPE && splits == 1 && a_mode == LOAD_K && b_mode != LOAD_S &&
         mm % PIPE_TALL_M == 0 && nn % PIPE_WIDE_N == 0 && k % (PIPE_STAGES * 16) == 0 &&
-        (t.tile == PIPE_TALL_M || t.slice_k == 32) &&
+        (t.tile == PIPE_TALL_M || (t.tile == GEMM_BM && t.slice_k == 32)) &&
         static_cast<uint64_t>(mm / PIPE_TALL_M) * (nn / PIPE_WIDE_N) * batch >= GEMM_CUS) {
         t.tile = PIPE_TALL_M;
         t.tile_n = PIPE_WIDE_N;

@@ -355,12 +355,11 @@ void launch_gemm_t(hipStream_t s, const GemmArgs& a, uint32_t groups) {
         if constexpr (AM != LOAD_S && BMD != LOAD_S) {
             const uint32_t last = a.k - (a.splits - 1) * a.k_chunk;
             if (a.tile == GEMM_SMALL_TILE) {
-                const uint32_t step = PIPE_KW * PIPE_STAGES * 16;
                 if (a.tile_n != GEMM_SMALL_TILE || a.m % GEMM_SMALL_TILE != 0 || a.n % GEMM_SMALL_TILE != 0 ||
-                    a.slice_k != 16 || a.k_chunk % step != 0 || last % step != 0) {
+                    a.slice_k != KW_BK || a.k_chunk % KW_STEP != 0 || last % KW_STEP != 0) {
                     fail_invalid("the K-split GEMM needs full 64x64 tiles and K chunks in whole steps");
                 }
-                hipLaunchKernelGGL((gemm_f32_kw<AM, BMD, 16, PIPE_STAGES>), dim3(groups), dim3(256), 0, s, a);
+                hipLaunchKernelGGL((gemm_f32_kw<AM, BMD, KW_BK, KW_STAGES>), dim3(groups), dim3(256), 0, s, a);
                 return;
             }
             const uint32_t step = PIPE_STAGES * a.slice_k;

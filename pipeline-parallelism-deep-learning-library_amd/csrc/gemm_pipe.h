@@ -593,7 +593,11 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_sk(GemmArgs p) {
 // gemm_f32_kw<AM, BMD, BK, NS>: a 64x64 output tile per workgroup whose four waves each
 // compute the whole tile (2x2 blocks of 32x32) over a quarter of the K chunk, through their own
 // NS LDS stages filled by their own direct loads: no barrier inside the loop (each wave waits
-// only for its own loads), the same in-wave pipelining as gemm_f32_pl. The four sums meet
+// only for its own loads), the same in-wave pipelining as gemm_f32_pl. Launched with two stages
+// of 32-deep slices: a slice's A loads go out in the first fragment group of the slice before
+// it, its B loads in the second, and each slice waits for all of them (1024^3 100.1-100.7 ->
+// 101.7-102.7 TFLOP/s, config 4 116 -> 117 against four stages of 16, A loads in one step's
+// first group and B loads in its last). With more stages the B loads go out in the last group. The four sums meet
 // through LDS at the end in a fixed order, (s0 + s1) + (s2 + s3), each wave adding and storing
 // one 32x32 block. One workgroup per compute unit (128 KB of stages): for grids of about one
 // 64x64 tile per compute unit (1024^3: 75 -> 97-99 TFLOP/s against four wave groups of four
@@ -660,9 +664,10 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
         issue_a(kt, stage);
         issue_b(kt, stage);
     };
-    // Loads issued after slice kt + 1's last one when step kt waits for it.
-    constexpr int AFTER = (NS - 3) * PER + GA::LOADS;
-    static_assert(NS >= 3, "A and B loads of a slice go out in different steps' groups");
+    constexpr bool TWO = NS == 2;  // two stages: B loads in the second group, wait for all
+    static_assert(!TWO || G >= 4, "two stages need four groups a slice");
+    constexpr int AFTER = TWO ? 0 : (NS - 3) * PER + GA::LOADS;
+    static_assert(TWO || NS >= 3, "A and B loads of a slice go out in different steps' groups");
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -697,12 +702,16 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
                 for (int g = 0; g + 1 < G; ++g) {
                     read((g + 1) & 1, g + 1, u);
                     if (g == 0) issue_a(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                    if (TWO && g == 1) issue_b(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
                     mfma_group<FM, FN>(acc, fa[g & 1], fb[g & 1]);
                     pl_after_each_mfma<RM, 0x100, RPM>();
                     if (g == 0) {
                         if constexpr (VF > 0) __builtin_amdgcn_sched_group_barrier(0x008, VF, 0);
                         pl_after_each_mfma<2, 0x010, VPM>();
                         __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - VF - 2, 0);
+                    } else if (TWO && g == 1) {
+                        pl_after_each_mfma<2, 0x010, VPM>();
+                        __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - 2, 0);
                     } else {
                         __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM, 0);
                     }
@@ -711,11 +720,11 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_kw(GemmArgs p) {
                 wait_vm<AFTER>();  // slice kt + 1 landed (this wave's own loads)
                 constexpr int L = (G - 1) & 1;
                 read(0, 0, (u + 1) % NS);
-                issue_b(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
+                if constexpr (!TWO) issue_b(min(kt + NS - 1, ktiles - 1), (u + NS - 1) % NS);
                 mfma_group<FM, FN>(acc, fa[L], fb[L]);
                 pl_after_each_mfma<RM, 0x100, RPM>();
-                pl_after_each_mfma<2, 0x010, VPM>();
-                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - 2, 0);
+                if constexpr (!TWO) pl_after_each_mfma<2, 0x010, VPM>();
+                __builtin_amdgcn_sched_group_barrier(0x008, 16 - RM - (TWO ? 0 : 2), 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }

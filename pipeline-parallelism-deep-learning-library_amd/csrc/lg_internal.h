@@ -151,6 +151,11 @@ constexpr uint32_t GEMM_WIDE_N = 256;
 // every chunk (K chunks in whole multiples of 4 * PIPE_STAGES * 16).
 constexpr uint32_t PIPE_STAGES = 4;
 constexpr uint32_t PIPE_KW = 4;  // waves splitting K on 64x64 tiles
+// gemm_f32_kw's slices and stages: two stages of 32-deep slices per wave, so a K chunk is a
+// whole number of KW_STEP (each of the PIPE_KW waves takes whole pairs of slices).
+constexpr uint32_t KW_BK = 32;
+constexpr uint32_t KW_STAGES = 2;
+constexpr uint32_t KW_STEP = PIPE_KW * KW_STAGES * KW_BK;
 constexpr uint32_t PIPE_NARROW_N = 64;  // N extent of the 128x64 pipelined tile
 constexpr uint32_t PIPE_TALL_M = 256;   // M extent of the 256x128 pipelined tile (gemm_f32_pl256)
 constexpr uint32_t PIPE_WIDE_N = 256;   // N extent of the 256x256 pipelined tile (gemm_f32_pl2x)
