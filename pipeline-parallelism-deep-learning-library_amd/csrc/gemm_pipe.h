@@ -595,9 +595,10 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_sk(GemmArgs p) {
 // NS LDS stages filled by their own direct loads: no barrier inside the loop (each wave waits
 // only for its own loads), the same in-wave pipelining as gemm_f32_pl. Launched with two stages
 // of 32-deep slices: a slice's A loads go out in the first fragment group of the slice before
-// it, its B loads in the second, and each slice waits for all of them (1024^3 100.1-100.7 ->
-// 101.7-102.7 TFLOP/s, config 4 116 -> 117 against four stages of 16, A loads in one step's
-// first group and B loads in its last). With more stages the B loads go out in the last group. The four sums meet
+// it, its B loads in the second, and each slice waits for all of them: every A row segment is
+// then a whole 128-byte line (against four stages of 16, A loads in one step's first group and B
+// loads in its last: 1024^3 and config 4 the same within 1-2 %). With more stages the B loads
+// go out in the last group. The four sums meet
 // through LDS at the end in a fixed order, (s0 + s1) + (s2 + s3), each wave adding and storing
 // one 32x32 block. One workgroup per compute unit (128 KB of stages): for grids of about one
 // 64x64 tile per compute unit (1024^3: 75 -> 97-99 TFLOP/s against four wave groups of four
