@@ -399,7 +399,7 @@ void gemm_f32_pl(GemmArgs p) {
 // per compute unit (96 KiB of stages). Every K in whole steps of NS slices; M a multiple of 256,
 // N of 128; no split.
 // Tiles are walked in groups of PL256_GROUP tile-rows: an XCD's 32 resident tiles then form a
-// 4 x 8 block, 1024 x 1024 of C, which reads the fewest A rows plus B columns per round (traffic
+// 4 x 8 block, 1024 x 1024 of C, which reads the fewest A rows plus B columns at a time (traffic
 // below the L2 on 4096^3: 3.0x the algorithmic bytes, against 3.7x in groups of 8).
 constexpr uint32_t PL256_GROUP = 4;
 template <int AM, int BMD, int BK, int NS>
